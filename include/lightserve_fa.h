@@ -1,0 +1,156 @@
+/*
+ * lightserve_fa.h -- C ABI of the gfx950 (MI355X) FlashAttention library
+ * (liblsfa_gfx950.so).
+ *
+ * This boundary replaces the Triton launches of lightserve's attention hot
+ * path. Every entry point takes plain device pointers, element strides and
+ * sizes (no framework types), enqueues work on the caller's stream, never
+ * allocates, frees or synchronises, and picks its kernel as a pure function
+ * of (dtype, head_dim, causal, varlen). That keeps it safe under stream/graph
+ * capture (the reference captures the forward inside torch.cuda.graph,
+ * model/cuda_graph_decode.py:137-139).
+ *
+ * Conventions shared by all entry points
+ *   - Layout of q/k/v/o/do/dq/dk/dv: [batch, heads, seqlen, head_dim] with
+ *     arbitrary element strides (index 0..3 = b, h, n, d), as the reference
+ *     passes all four strides per tensor (kernels/flash_attention.py:211-218).
+ *     The fast path requires stride[3] == 1, the other strides and head_dim to
+ *     be multiples of 8 elements, and 16-byte aligned base pointers; other
+ *     layouts are rejected with LSFA_ERR_UNSUPPORTED (the Python layer makes
+ *     a packed copy first).
+ *   - Varlen ("packed THD") mode: cu_seqlens_q / cu_seqlens_k are device
+ *     int32 arrays of batch+1 prefix offsets. Tensors are then [total_tokens,
+ *     heads, head_dim]; stride[0] is ignored, stride[1] is the head stride and
+ *     stride[2] the token stride. seqlen_q / seqlen_k give the maximum
+ *     per-sequence lengths. lse is [heads, total_q] (lse_stride[1] = head
+ *     stride, lse_stride[2] = token stride).
+ *   - Causal masking is bottom-right aligned: query i of a sequence with
+ *     Nq queries and Nk keys sees keys j <= i + (Nk - Nq). With Nq == Nk this
+ *     is the reference's `offs_m >= offs_n` (kernels/flash_attention.py:152).
+ *   - Scores are S = (q . k) * sm_scale in fp32; lse = m + ln(l) per query row
+ *     in natural-log, scaled-score units (kernels/flash_attention_backward.py:162).
+ *     A row that sees no key gets o = 0 and lse = -inf.
+ *   - GQA: query head h reads kv head h / (heads_q / heads_kv).
+ *   - Return value: LSFA_OK (0) or a negative lsfa_status; the message of the
+ *     last failure on the calling thread is returned by lsfa_last_error().
+ */
+#ifndef LIGHTSERVE_FA_H
+#define LIGHTSERVE_FA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LSFA_ABI_VERSION 1
+
+typedef enum {
+  LSFA_DTYPE_FP32 = 0,
+  LSFA_DTYPE_FP16 = 1,
+  LSFA_DTYPE_BF16 = 2
+} lsfa_dtype;
+
+typedef enum {
+  LSFA_OK = 0,
+  LSFA_ERR_INVALID = -1,     /* malformed arguments (null pointer, bad sizes) */
+  LSFA_ERR_UNSUPPORTED = -2, /* valid but outside what the kernels implement */
+  LSFA_ERR_LAUNCH = -3       /* the HIP runtime refused the launch */
+} lsfa_status;
+
+/* Forward arguments. lse may be NULL (inference forward, which the reference
+ * returns without logsumexp: kernels/flash_attention.py:182-222). */
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t o_stride[4];
+  int64_t lse_stride[3];
+  const int32_t* cu_seqlens_q; /* NULL unless varlen */
+  const int32_t* cu_seqlens_k; /* NULL unless varlen */
+  int32_t dtype;               /* lsfa_dtype; q, k, v and o share it */
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t seqlen_q;            /* varlen: max_seqlen_q */
+  int32_t seqlen_k;            /* varlen: max_seqlen_k */
+  int32_t head_dim;            /* 1..128 */
+  int32_t causal;
+  float sm_scale;
+  int32_t reserved;
+} lsfa_fwd_args;
+
+/* Backward arguments. delta is a caller-allocated fp32 workspace shaped like
+ * lse (rowsum(dO * O), kernels/flash_attention_backward.py:202-229); the
+ * library writes it before using it. dq/dk/dv are written in the input dtype
+ * (no fp32 dq staging buffer and no atomics: dq is produced by its own
+ * query-stationary kernel, so results are deterministic). */
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  const float* lse;
+  void* dq;
+  void* dk;
+  void* dv;
+  float* delta;
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t o_stride[4];
+  int64_t do_stride[4];
+  int64_t dq_stride[4];
+  int64_t dk_stride[4];
+  int64_t dv_stride[4];
+  int64_t lse_stride[3];       /* shared by lse and delta */
+  const int32_t* cu_seqlens_q; /* must be NULL: varlen backward is not implemented */
+  const int32_t* cu_seqlens_k;
+  int32_t dtype;
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;            /* must equal heads_q: GQA backward is not implemented */
+  int32_t seqlen_q;
+  int32_t seqlen_k;
+  int32_t head_dim;
+  int32_t causal;
+  float sm_scale;
+  int32_t reserved;
+} lsfa_bwd_args;
+
+/* ABI version of the loaded library (LSFA_ABI_VERSION). */
+int lsfa_abi_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* lsfa_last_error(void);
+
+/* Host-only validation of forward arguments; never touches the GPU.
+ * Mirrors the reference's argument checks (kernels/flash_attention.py:192-199)
+ * plus the layout requirements of the gfx950 kernels. */
+int lsfa_fwd_check(const lsfa_fwd_args* args);
+
+/* Forward: o = softmax(q k^T * sm_scale) v, and lse if requested.
+ * Replaces the launch of _flash_attn_fwd_kernel (kernels/flash_attention.py:210-221)
+ * and of _flash_attn_fwd_lse_kernel (kernels/flash_attention_backward.py:186-198).
+ * stream is a hipStream_t (NULL = the default stream). */
+int lsfa_fwd(const lsfa_fwd_args* args, void* stream);
+
+/* Host-only validation of backward arguments; never touches the GPU. */
+int lsfa_bwd_check(const lsfa_bwd_args* args);
+
+/* Backward: delta, then dq, dk, dv. Replaces the preprocess launch
+ * (kernels/flash_attention_backward.py:341-350), the backward launch
+ * (:363-381) and the fp32->dtype cast of dq (:382). */
+int lsfa_bwd(const lsfa_bwd_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIGHTSERVE_FA_H */

@@ -1,0 +1,151 @@
+"""ctypes binding of liblsfa_gfx950.so (declared in include/lightserve_fa.h).
+
+The library is loaded lazily, once, under a lock: importing the package needs
+neither the library nor a GPU, so argument validation (AssertionError, as in
+the reference) runs in CPU-only processes. Calls that reach the library on a
+machine where it is missing raise RuntimeError; there is no fallback path.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+_LIB_NAME = "liblsfa_gfx950.so"
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
+ABI_VERSION = 1
+
+DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
+TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}
+
+STATUS = {0: "LSFA_OK", -1: "LSFA_ERR_INVALID", -2: "LSFA_ERR_UNSUPPORTED", -3: "LSFA_ERR_LAUNCH"}
+
+EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "lsfa_fwd",
+                    "lsfa_bwd_check", "lsfa_bwd")
+
+_i64x4 = ctypes.c_int64 * 4
+_i64x3 = ctypes.c_int64 * 3
+
+
+class FwdArgs(ctypes.Structure):
+    """Mirror of lsfa_fwd_args."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("q_stride", _i64x4), ("k_stride", _i64x4), ("v_stride", _i64x4), ("o_stride", _i64x4),
+        ("lse_stride", _i64x3),
+        ("cu_seqlens_q", ctypes.c_void_p), ("cu_seqlens_k", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32), ("seqlen_q", ctypes.c_int32), ("seqlen_k", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("causal", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class BwdArgs(ctypes.Structure):
+    """Mirror of lsfa_bwd_args."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("dout", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p), ("dk", ctypes.c_void_p), ("dv", ctypes.c_void_p),
+        ("delta", ctypes.c_void_p),
+        ("q_stride", _i64x4), ("k_stride", _i64x4), ("v_stride", _i64x4), ("o_stride", _i64x4),
+        ("do_stride", _i64x4), ("dq_stride", _i64x4), ("dk_stride", _i64x4), ("dv_stride", _i64x4),
+        ("lse_stride", _i64x3),
+        ("cu_seqlens_q", ctypes.c_void_p), ("cu_seqlens_k", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32), ("seqlen_q", ctypes.c_int32), ("seqlen_k", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("causal", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library_path():
+    return _LIB_PATH
+
+
+def load():
+    """Returns the loaded library, loading it on first use."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"{_LIB_NAME} is not built ({_LIB_PATH} missing); run "
+                "`python -m lightserve_amd.csrc.build` (or __graft_entry__.build()) first")
+        lib = ctypes.CDLL(_LIB_PATH)
+        lib.lsfa_abi_version.restype = ctypes.c_int
+        lib.lsfa_abi_version.argtypes = []
+        lib.lsfa_last_error.restype = ctypes.c_char_p
+        lib.lsfa_last_error.argtypes = []
+        for name, struct in (("lsfa_fwd_check", FwdArgs), ("lsfa_bwd_check", BwdArgs)):
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(struct)]
+        for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs)):
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
+        version = lib.lsfa_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{_LIB_NAME} has ABI version {version}, expected {ABI_VERSION}")
+        _lib = lib
+        return _lib
+
+
+def _raise_on(rc, what):
+    if rc != 0:
+        msg = load().lsfa_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {STATUS.get(rc, rc)}: {msg}")
+
+
+def fwd_check(args):
+    """Host-only validation (no GPU access); returns (status, message)."""
+    lib = load()
+    rc = lib.lsfa_fwd_check(ctypes.byref(args))
+    return rc, lib.lsfa_last_error().decode(errors="replace")
+
+
+def bwd_check(args):
+    lib = load()
+    rc = lib.lsfa_bwd_check(ctypes.byref(args))
+    return rc, lib.lsfa_last_error().decode(errors="replace")
+
+
+def fwd(args, stream):
+    _raise_on(load().lsfa_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_fwd")
+
+
+def bwd(args, stream):
+    _raise_on(load().lsfa_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_bwd")
+
+
+def strides4(t):
+    """Element strides of a [b, h, n, d] tensor."""
+    return _i64x4(*t.stride())
+
+
+def strides_thd(t):
+    """Element strides of a packed [tokens, heads, d] tensor in ABI order (b, h, n, d)."""
+    st = t.stride()
+    return _i64x4(0, st[1], st[0], st[2])
+
+
+def fast_layout_ok(t):
+    """Whether the bf16/fp16 kernels can address t in place: unit head-dim
+    stride, head_dim and every other stride a multiple of 8 elements, 16-byte
+    aligned base (the requirements lsfa_fwd_check/lsfa_bwd_check enforce)."""
+    if t.stride(-1) != 1 or t.shape[-1] % 8 != 0 or t.data_ptr() % 16 != 0:
+        return False
+    return all(s % 8 == 0 for s in t.stride()[:-1])
+
+
+def current_stream(device):
+    return torch.cuda.current_stream(device).cuda_stream

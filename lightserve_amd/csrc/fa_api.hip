@@ -1,0 +1,187 @@
+// C ABI of liblsfa_gfx950.so: argument validation (host only, no GPU access)
+// and kernel selection. See include/lightserve_fa.h for the contract.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/lightserve_fa.h"
+#include "fa_common.hpp"
+
+namespace lsfa {
+hipError_t fwd_mfma(FwdParams p, bool is_bf16, int dp, bool causal, bool varlen, hipStream_t s);
+hipError_t bwd_mfma(const BwdParams& p, bool is_bf16, int dp, bool causal, hipStream_t s);
+hipError_t fwd_f32(const FwdParams& p, int dp, bool causal, bool varlen, float scale, hipStream_t s);
+hipError_t bwd_f32(const BwdParams& p, int dp, bool causal, hipStream_t s);
+}  // namespace lsfa
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return LSFA_OK;
+}
+
+// Padded head dim of the kernels: 32, 64 or 128.
+int padded_dim(int d) { return d <= 32 ? 32 : (d <= 64 ? 64 : 128); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Layout requirement of the MFMA kernels for one [b, h, n, d] tensor.
+int check_fast_layout(const char* name, const void* ptr, const int64_t* st, bool varlen) {
+  if (st[3] != 1) return fail(LSFA_ERR_UNSUPPORTED, "%s: head-dim stride must be 1 for bf16/fp16 (got %lld)", name, (long long)st[3]);
+  for (int i = varlen ? 1 : 0; i < 3; ++i)
+    if (st[i] % 8 != 0)
+      return fail(LSFA_ERR_UNSUPPORTED, "%s: stride[%d]=%lld is not a multiple of 8 elements", name, i, (long long)st[i]);
+  if (!aligned16(ptr)) return fail(LSFA_ERR_UNSUPPORTED, "%s: base pointer is not 16-byte aligned", name);
+  return LSFA_OK;
+}
+
+int check_common(int dtype, int batch, int hq, int hkv, int nq, int nk, int d, float scale) {
+  if (dtype != LSFA_DTYPE_FP32 && dtype != LSFA_DTYPE_FP16 && dtype != LSFA_DTYPE_BF16)
+    return fail(LSFA_ERR_INVALID, "unknown dtype %d", dtype);
+  if (batch < 0 || hq < 0 || hkv < 0 || nq < 0 || nk < 0)
+    return fail(LSFA_ERR_INVALID, "negative size (batch=%d heads_q=%d heads_kv=%d seqlen_q=%d seqlen_k=%d)", batch, hq,
+                hkv, nq, nk);
+  if (hkv == 0 && hq != 0) return fail(LSFA_ERR_INVALID, "heads_kv must be positive");
+  if (hkv > 0 && hq % hkv != 0) return fail(LSFA_ERR_INVALID, "heads_q (%d) is not a multiple of heads_kv (%d)", hq, hkv);
+  if (d < 1 || d > 128) return fail(LSFA_ERR_UNSUPPORTED, "head_dim %d outside 1..128", d);
+  if (!std::isfinite(scale)) return fail(LSFA_ERR_INVALID, "sm_scale is not finite");
+  const long long tiles = (long long)((nq + 63) / 64) * batch * hq;
+  if (tiles > (1LL << 30)) return fail(LSFA_ERR_UNSUPPORTED, "problem too large for one launch");
+  return LSFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lsfa_abi_version(void) { return LSFA_ABI_VERSION; }
+
+const char* lsfa_last_error(void) { return g_last_error.c_str(); }
+
+int lsfa_fwd_check(const lsfa_fwd_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  int rc = check_common(a->dtype, a->batch, a->heads_q, a->heads_kv, a->seqlen_q, a->seqlen_k, a->head_dim, a->sm_scale);
+  if (rc) return rc;
+  if ((a->cu_seqlens_q == nullptr) != (a->cu_seqlens_k == nullptr))
+    return fail(LSFA_ERR_INVALID, "cu_seqlens_q and cu_seqlens_k must both be set or both be NULL");
+  const bool empty = (long long)a->batch * a->heads_q * a->seqlen_q == 0;
+  if (!empty && (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->o == nullptr))
+    return fail(LSFA_ERR_INVALID, "q, k, v and o must be non-NULL");
+  const bool varlen = a->cu_seqlens_q != nullptr;
+  if (a->dtype != LSFA_DTYPE_FP32 && !empty) {
+    if (a->head_dim % 8 != 0)
+      return fail(LSFA_ERR_UNSUPPORTED, "bf16/fp16 head_dim must be a multiple of 8 (got %d)", a->head_dim);
+    if ((rc = check_fast_layout("q", a->q, a->q_stride, varlen))) return rc;
+    if ((rc = check_fast_layout("k", a->k, a->k_stride, varlen))) return rc;
+    if ((rc = check_fast_layout("v", a->v, a->v_stride, varlen))) return rc;
+    if ((rc = check_fast_layout("o", a->o, a->o_stride, varlen))) return rc;
+  }
+  return ok();
+}
+
+int lsfa_fwd(const lsfa_fwd_args* a, void* stream) {
+  int rc = lsfa_fwd_check(a);
+  if (rc) return rc;
+  if ((long long)a->batch * a->heads_q * a->seqlen_q == 0) return ok();
+  lsfa::FwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = a->q;
+  p.k = a->k;
+  p.v = a->v;
+  p.o = a->o;
+  p.lse = a->lse;
+  p.sqb = a->q_stride[0]; p.sqh = a->q_stride[1]; p.sqn = a->q_stride[2]; p.sqd = a->q_stride[3];
+  p.skb = a->k_stride[0]; p.skh = a->k_stride[1]; p.skn = a->k_stride[2]; p.skd = a->k_stride[3];
+  p.svb = a->v_stride[0]; p.svh = a->v_stride[1]; p.svn = a->v_stride[2]; p.svd = a->v_stride[3];
+  p.sob = a->o_stride[0]; p.soh = a->o_stride[1]; p.son = a->o_stride[2]; p.sod = a->o_stride[3];
+  p.slb = a->lse_stride[0]; p.slh = a->lse_stride[1]; p.sln = a->lse_stride[2];
+  p.cu_q = a->cu_seqlens_q;
+  p.cu_k = a->cu_seqlens_k;
+  p.B = a->batch; p.Hq = a->heads_q; p.Hkv = a->heads_kv;
+  p.Nq = a->seqlen_q; p.Nk = a->seqlen_k; p.D = a->head_dim;
+  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  const bool varlen = a->cu_seqlens_q != nullptr;
+  const int dp = padded_dim(a->head_dim);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (a->dtype == LSFA_DTYPE_FP32)
+    e = lsfa::fwd_f32(p, dp, a->causal != 0, varlen, a->sm_scale, s);
+  else
+    e = lsfa::fwd_mfma(p, a->dtype == LSFA_DTYPE_BF16, dp, a->causal != 0, varlen, s);
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int lsfa_bwd_check(const lsfa_bwd_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  int rc = check_common(a->dtype, a->batch, a->heads_q, a->heads_kv, a->seqlen_q, a->seqlen_k, a->head_dim, a->sm_scale);
+  if (rc) return rc;
+  if (a->cu_seqlens_q != nullptr || a->cu_seqlens_k != nullptr)
+    return fail(LSFA_ERR_UNSUPPORTED, "varlen backward is not implemented");
+  if (a->heads_kv != a->heads_q) return fail(LSFA_ERR_UNSUPPORTED, "GQA backward is not implemented (heads_kv != heads_q)");
+  const bool empty = (long long)a->batch * a->heads_q * (a->seqlen_q + a->seqlen_k) == 0;
+  if (!empty) {
+    if (!a->q || !a->k || !a->v || !a->o || !a->dout || !a->lse || !a->dq || !a->dk || !a->dv || !a->delta)
+      return fail(LSFA_ERR_INVALID, "q, k, v, o, dout, lse, dq, dk, dv and delta must be non-NULL");
+    if (a->dtype != LSFA_DTYPE_FP32) {
+      if (a->head_dim % 8 != 0)
+        return fail(LSFA_ERR_UNSUPPORTED, "bf16/fp16 head_dim must be a multiple of 8 (got %d)", a->head_dim);
+      const char* names[8] = {"q", "k", "v", "o", "dout", "dq", "dk", "dv"};
+      const void* ptrs[8] = {a->q, a->k, a->v, a->o, a->dout, a->dq, a->dk, a->dv};
+      const int64_t* strides[8] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride,
+                                   a->do_stride, a->dq_stride, a->dk_stride, a->dv_stride};
+      for (int i = 0; i < 8; ++i)
+        if ((rc = check_fast_layout(names[i], ptrs[i], strides[i], false))) return rc;
+    }
+  }
+  return ok();
+}
+
+int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
+  int rc = lsfa_bwd_check(a);
+  if (rc) return rc;
+  if ((long long)a->batch * a->heads_q * (a->seqlen_q + a->seqlen_k) == 0) return ok();
+  lsfa::BwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.dout = a->dout; p.lse = a->lse;
+  p.dq = a->dq; p.dk = a->dk; p.dv = a->dv; p.delta = a->delta;
+  p.sqb = a->q_stride[0]; p.sqh = a->q_stride[1]; p.sqn = a->q_stride[2]; p.sqd = a->q_stride[3];
+  p.skb = a->k_stride[0]; p.skh = a->k_stride[1]; p.skn = a->k_stride[2]; p.skd = a->k_stride[3];
+  p.svb = a->v_stride[0]; p.svh = a->v_stride[1]; p.svn = a->v_stride[2]; p.svd = a->v_stride[3];
+  p.sob = a->o_stride[0]; p.soh = a->o_stride[1]; p.son = a->o_stride[2]; p.sod = a->o_stride[3];
+  p.sdob = a->do_stride[0]; p.sdoh = a->do_stride[1]; p.sdon = a->do_stride[2]; p.sdod = a->do_stride[3];
+  p.sdqb = a->dq_stride[0]; p.sdqh = a->dq_stride[1]; p.sdqn = a->dq_stride[2]; p.sdqd = a->dq_stride[3];
+  p.sdkb = a->dk_stride[0]; p.sdkh = a->dk_stride[1]; p.sdkn = a->dk_stride[2]; p.sdkd = a->dk_stride[3];
+  p.sdvb = a->dv_stride[0]; p.sdvh = a->dv_stride[1]; p.sdvn = a->dv_stride[2]; p.sdvd = a->dv_stride[3];
+  p.slb = a->lse_stride[0]; p.slh = a->lse_stride[1]; p.sln = a->lse_stride[2];
+  p.B = a->batch; p.H = a->heads_q; p.Nq = a->seqlen_q; p.Nk = a->seqlen_k; p.D = a->head_dim;
+  p.scale = a->sm_scale;
+  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  const int dp = padded_dim(a->head_dim);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (a->dtype == LSFA_DTYPE_FP32)
+    e = lsfa::bwd_f32(p, dp, a->causal != 0, s);
+  else
+    e = lsfa::bwd_mfma(p, a->dtype == LSFA_DTYPE_BF16, dp, a->causal != 0, s);
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"

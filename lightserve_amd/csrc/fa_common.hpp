@@ -1,0 +1,164 @@
+// Shared device-side helpers for the gfx950 FlashAttention kernels.
+//
+// Register layouts used throughout (checked on MI355X with an in-bounds lane
+// probe of the builtins):
+//   v_mfma_f32_32x32x16_{bf16,f16}  C[32x32] += A[32x16] * B[16x32]
+//     A: lane l holds A[l%32][8*(l/32) + s], s = 0..7
+//     B: lane l holds B[8*(l/32) + s][l%32]
+//     C: lane l, register i holds C[8*(i/4) + 4*(l/32) + i%4][l%32]
+//   ds_read_b64_tr_b16: inside each group of 16 lanes, lane 4r+e receives, in
+//     slot j, element e of the 8 bytes addressed by lane 4j+r of the group.
+//   v_permlane32_swap(a, b): lanes 32..63 of a trade places with lanes 0..31
+//     of b, so max(r[0], r[1]) of swap(x, x) reduces x across the two halves.
+//
+// Every kernel computes transposed score tiles S^T = K Q^T (or S = Q K^T in the
+// key-stationary backward) so that an accumulator can be converted in
+// registers into the B operand of the next MFMA; the matching A operand is
+// then read from LDS with the transpose read above.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lsfa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define LDS_AS __attribute__((address_space(3)))
+
+template <typename T> struct VecT;
+template <> struct VecT<__bf16> { using x8 = bf16x8; using x4 = bf16x4; };
+template <> struct VecT<_Float16> { using x8 = f16x8; using x4 = f16x4; };
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Transposed 8-byte LDS read (see header comment for the lane mapping).
+__device__ __forceinline__ bf16x4 lds_read_tr(const LDS_AS __bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4*)p);
+}
+typedef __fp16 fp16x4_builtin __attribute__((__vector_size__(4 * sizeof(__fp16))));
+__device__ __forceinline__ f16x4 lds_read_tr(const LDS_AS _Float16* p) {
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS fp16x4_builtin*)p));
+}
+
+template <typename T>
+__device__ __forceinline__ typename VecT<T>::x8 lds_read8(const LDS_AS T* p) {
+  return *(const LDS_AS typename VecT<T>::x8*)p;
+}
+
+template <typename X8, typename X4>
+__device__ __forceinline__ X8 cat4(X4 a, X4 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Eight consecutive accumulator registers -> one bf16/f16 MFMA operand (RNE).
+template <typename T>
+__device__ __forceinline__ typename VecT<T>::x8 pack8(const f32x16& c, int base) {
+  typename VecT<T>::x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = (T)c[base + s];
+  return r;
+}
+
+// All-reduce across the two 32-lane halves of a wave.
+__device__ __forceinline__ float half_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 16-byte segment swizzle of LDS tiles stored [rows][DP]. Rows r..r+15 read
+// at one segment (K operand, ds_read_b128) and 4x4 blocks of (row, segment)
+// (transpose reads) both land on distinct bank groups.
+template <int DP>
+__device__ __forceinline__ int seg_swz(int row) {
+  return (((row & 3) << 2) | ((row >> 2) & 3)) & (DP / 8 - 1);
+}
+// Element offset of (row, col) inside a swizzled [rows][DP] LDS tile; col%8
+// is preserved, so 8- and 16-byte accesses stay contiguous.
+template <int DP>
+__device__ __forceinline__ int swz_off(int row, int col) {
+  return row * DP + ((((col >> 3) ^ seg_swz<DP>(row))) << 3) + (col & 7);
+}
+
+// Kernel-side argument block (filled by the host dispatcher from the C ABI
+// structs; all strides in elements).
+struct FwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int64_t sqb, sqh, sqn;
+  int64_t skb, skh, skn;
+  int64_t svb, svh, svn;
+  int64_t sob, soh, son;
+  int64_t slb, slh, sln;
+  int64_t sqd, skd, svd, sod;  // head-dim strides (fp32 path only; 1 on the MFMA path)
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int B, Hq, Hkv, Nq, Nk, D;
+  int num_q_tiles;
+  float scale_log2;  // sm_scale * log2(e)
+};
+
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  const float* lse;
+  void* dq;
+  void* dk;
+  void* dv;
+  float* delta;
+  int64_t sqb, sqh, sqn;
+  int64_t skb, skh, skn;
+  int64_t svb, svh, svn;
+  int64_t sob, soh, son;
+  int64_t sdob, sdoh, sdon;
+  int64_t sdqb, sdqh, sdqn;
+  int64_t sdkb, sdkh, sdkn;
+  int64_t sdvb, sdvh, sdvn;
+  int64_t slb, slh, sln;
+  int64_t sqd, skd, svd, sod, sdod, sdqd, sdkd, sdvd;  // fp32 path only
+  int B, H, Nq, Nk, D;
+  int num_tiles;     // tiles per (b, h) along the kernel's stationary axis
+  float scale;       // sm_scale
+  float scale_log2;  // sm_scale * log2(e)
+};
+
+// Maps the 1-D launch index to (batch*head, tile). Workgroups are handed to
+// the 8 XCDs round-robin by launch index, so consecutive launch indices are
+// spread so that each XCD owns a contiguous run of heads (their K/V stay in
+// that XCD's L2), and within a head the tiles are issued heaviest-first
+// (largest causal extent first) for load balance.
+__device__ __forceinline__ void map_tile(int num_tiles, int total, int& bh, int& tile, bool heavy_last_index) {
+  const int L = blockIdx.x;
+  int W = L;
+  if ((total & 7) == 0) W = (L & 7) * (total >> 3) + (L >> 3);
+  bh = W / num_tiles;
+  const int t = W - bh * num_tiles;
+  tile = heavy_last_index ? (num_tiles - 1 - t) : t;
+}
+
+__device__ __forceinline__ u32x4 ldg16(const void* p) { return *(const u32x4*)p; }
+
+}  // namespace lsfa

@@ -1,0 +1,25 @@
+"""CPU oracle for the FlashAttention hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this package, and only as the checker (or, for bench.py, as the timed CPU
+baseline). The product path (lightserve_amd) never imports it: with the HIP
+library missing it raises instead of falling back to anything here.
+
+Contents
+  attention.py  closed-form attention in float64 (the reference's test oracle,
+                kernels/tests/test_flash_attention.py:47), its autograd
+                gradients, a line-by-line restatement of the reference's
+                tiled forward/backward loops, varlen/GQA, and a pure-Python
+                loop version for tiny inputs.
+  inputs.py     the seeded input recipe of the five BASELINE configurations.
+
+How each function is pinned (tests/test_oracle.py):
+  attention_reference   pure-Python loops (golden fixtures under tests/golden),
+                        closed-form invariants, torch SDPA in float64.
+  attention_grads       float64 gradcheck (calculus) and the restated backward.
+  flash_forward_tiled   attention_reference (fp32 operands: 1e-6).
+  flash_backward_tiled  attention_grads (fp32 operands: 1e-6).
+  varlen_reference      pure-Python loops with GQA and bottom-right masking.
+Every function has at least one check that a planted mistake (a dropped
+scale, a transposed operand, a wrong mask offset) fails.
+"""

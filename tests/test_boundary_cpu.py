@@ -1,0 +1,180 @@
+"""CPU-only checks of the drop-in boundary: the reference's validation tests
+(kernels/tests/test_flash_attention.py:80-122,
+kernels/tests/test_flash_attention_backward.py:127-139) against the new entry
+points, and the C ABI library loading, exporting every declared symbol, and
+rejecting bad arguments on the host (no GPU call is made here)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from lightserve_amd import _lib
+from lightserve_amd.kernels.flash_attention import flash_attention_forward
+from lightserve_amd.kernels.flash_attention_backward import flash_attention
+from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen_forward
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "lightserve_fa.h")
+
+ENTRY_POINTS = [flash_attention_forward, flash_attention]
+
+
+@pytest.mark.parametrize("fn", ENTRY_POINTS)
+def test_rejects_shape_mismatch(fn):
+    q = torch.randn(1, 2, 16, 32)
+    k = torch.randn(1, 2, 16, 32)
+    v = torch.randn(1, 2, 8, 32)
+    with pytest.raises(AssertionError):
+        fn(q, k, v)
+
+
+@pytest.mark.parametrize("fn", ENTRY_POINTS)
+def test_rejects_dtype_mismatch(fn):
+    q = torch.randn(1, 2, 16, 32, dtype=torch.float32)
+    k = torch.randn(1, 2, 16, 32, dtype=torch.float16)
+    v = torch.randn(1, 2, 16, 32, dtype=torch.float32)
+    with pytest.raises(AssertionError):
+        fn(q, k, v)
+
+
+@pytest.mark.parametrize("fn", ENTRY_POINTS)
+def test_rejects_wrong_ndim(fn):
+    q = torch.randn(2, 16, 32)
+    with pytest.raises(AssertionError):
+        fn(q, q, q)
+
+
+@pytest.mark.parametrize("fn", ENTRY_POINTS)
+def test_rejects_cpu_tensor(fn):
+    q = torch.randn(1, 2, 16, 32)
+    with pytest.raises(AssertionError):
+        fn(q, q.clone(), q.clone())
+
+
+@pytest.mark.parametrize("fn", ENTRY_POINTS)
+def test_rejects_head_dim_mismatch(fn):
+    q = torch.randn(1, 2, 16, 32)
+    v = torch.randn(1, 2, 16, 64)
+    with pytest.raises(AssertionError):
+        fn(q, q, v)
+
+
+def test_varlen_validation():
+    q = torch.randn(8, 4, 16)
+    k = torch.randn(10, 2, 16)
+    cu = torch.tensor([0, 8], dtype=torch.int32)
+    with pytest.raises(AssertionError):  # CPU tensors
+        flash_attention_varlen_forward(q, k, k, cu, torch.tensor([0, 10], dtype=torch.int32), 8, 10)
+    with pytest.raises(AssertionError):  # heads not a multiple
+        flash_attention_varlen_forward(q, torch.randn(10, 3, 16), torch.randn(10, 3, 16), cu, cu, 8, 10)
+    with pytest.raises(AssertionError):  # 4-D input
+        flash_attention_varlen_forward(q[None], k, k, cu, cu, 8, 10)
+
+
+def test_import_loads_no_native_code():
+    """Importing the package must not need the library or a GPU (the
+    reference's CI runs validation tests on CPU-only runners)."""
+    import subprocess
+    import sys
+    code = ("import lightserve_amd.kernels, lightserve_amd._lib as L, sys; "
+            "sys.exit(0 if L._lib is None else 1)")
+    assert subprocess.run([sys.executable, "-c", code], cwd=os.path.dirname(HEADER) + "/..").returncode == 0
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(lsfa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol(built_library):
+    declared = _declared_functions()
+    assert set(declared) == set(_lib.EXPORTED_SYMBOLS)
+    lib = ctypes.CDLL(built_library)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert _lib.load().lsfa_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layout_matches_header(built_library):
+    """ctypes mirrors must have the C struct sizes (checked with the
+    host compiler against the header)."""
+    import shutil
+    import subprocess
+    import tempfile
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no host C compiler")
+    src = ('#include <stdio.h>\n#include <stddef.h>\n#include "lightserve_fa.h"\n'
+           'int main(void){printf("%zu %zu %zu %zu\\n", sizeof(lsfa_fwd_args), sizeof(lsfa_bwd_args),'
+           ' offsetof(lsfa_fwd_args, sm_scale), offsetof(lsfa_bwd_args, sm_scale)); return 0;}\n')
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "t.c")
+        exe = os.path.join(d, "t")
+        open(c, "w").write(src)
+        subprocess.run([cc, "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
+        sizes = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    assert sizes == [ctypes.sizeof(_lib.FwdArgs), ctypes.sizeof(_lib.BwdArgs),
+                     _lib.FwdArgs.sm_scale.offset, _lib.BwdArgs.sm_scale.offset]
+
+
+def _fwd_args(**kw):
+    st = _lib._i64x4(8 * 4 * 64, 8 * 64, 64, 1)
+    base = dict(q=16, k=32, v=48, o=64, lse=None, q_stride=st, k_stride=st, v_stride=st, o_stride=st,
+                lse_stride=_lib._i64x3(32, 8, 1), cu_seqlens_q=None, cu_seqlens_k=None,
+                dtype=_lib.DTYPE_BF16, batch=1, heads_q=4, heads_kv=4, seqlen_q=8, seqlen_k=8,
+                head_dim=64, causal=1, sm_scale=0.125, reserved=0)
+    base.update(kw)
+    return _lib.FwdArgs(**base)
+
+
+def test_abi_host_validation(built_library):
+    """Host-only validation paths; fake (never dereferenced) pointers."""
+    assert _lib.fwd_check(_fwd_args())[0] == 0
+    rc, msg = _lib.fwd_check(_fwd_args(dtype=7))
+    assert rc == -1 and "dtype" in msg
+    rc, msg = _lib.fwd_check(_fwd_args(head_dim=256))
+    assert rc == -2 and "head_dim" in msg
+    rc, msg = _lib.fwd_check(_fwd_args(heads_q=6, heads_kv=4))
+    assert rc == -1 and "multiple" in msg
+    rc, msg = _lib.fwd_check(_fwd_args(q=None))
+    assert rc == -1 and "non-NULL" in msg
+    rc, msg = _lib.fwd_check(_fwd_args(q=18))
+    assert rc == -2 and "aligned" in msg
+    rc, msg = _lib.fwd_check(_fwd_args(q_stride=_lib._i64x4(2048, 512, 64, 2)))
+    assert rc == -2 and "stride" in msg
+    rc, msg = _lib.fwd_check(_fwd_args(cu_seqlens_q=16))
+    assert rc == -1 and "cu_seqlens" in msg
+    rc, msg = _lib.fwd_check(_fwd_args(sm_scale=float("nan")))
+    assert rc == -1 and "sm_scale" in msg
+    # fp32 accepts any stride and head dim up to 128
+    assert _lib.fwd_check(_fwd_args(dtype=_lib.DTYPE_FP32, head_dim=12, q=18,
+                                    q_stride=_lib._i64x4(7, 5, 3, 2)))[0] == 0
+    # the launching entry point validates first and never reaches the GPU on bad input
+    with pytest.raises(RuntimeError, match="LSFA_ERR_INVALID"):
+        _lib.fwd(_fwd_args(batch=-1), 0)
+    # empty problems are a successful no-op
+    _lib.fwd(_fwd_args(seqlen_q=0, q=None, k=None, v=None, o=None), 0)
+
+
+def test_abi_backward_validation(built_library):
+    st = _lib._i64x4(2048, 512, 64, 1)
+    args = _lib.BwdArgs(q=16, k=32, v=48, o=64, dout=80, lse=96, dq=112, dk=128, dv=144, delta=160,
+                        q_stride=st, k_stride=st, v_stride=st, o_stride=st, do_stride=st, dq_stride=st,
+                        dk_stride=st, dv_stride=st, lse_stride=_lib._i64x3(32, 8, 1),
+                        cu_seqlens_q=None, cu_seqlens_k=None, dtype=_lib.DTYPE_BF16, batch=1,
+                        heads_q=4, heads_kv=4, seqlen_q=8, seqlen_k=8, head_dim=64, causal=1,
+                        sm_scale=0.125, reserved=0)
+    assert _lib.bwd_check(args)[0] == 0
+    args.heads_kv = 2
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -2 and "GQA" in msg
+    args.heads_kv = 4
+    args.delta = None
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -1
+    args.delta = 160
+    args.cu_seqlens_q = 16
+    args.cu_seqlens_k = 32
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -2 and "varlen" in msg

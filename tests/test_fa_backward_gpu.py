@@ -1,0 +1,109 @@
+"""GPU parity of the backward kernels against the oracle's gradients.
+
+Mirrors the reference's backward tests
+(kernels/tests/test_flash_attention_backward.py: gradcheck :44-65, gradients
+vs autograd :68-104, forward-with-LSE vs forward-only :107-124) with the
+oracle's autograd (float64 on the CPU, or fp32 on the GPU for full-size
+configs) in place of SDPA, and adds the BASELINE gate at config sizes,
+determinism and odd strides of dO.
+"""
+import pytest
+import torch
+
+from lightserve_amd.kernels.flash_attention import flash_attention_forward
+from lightserve_amd.kernels.flash_attention_backward import (_flash_attention_backward, _flash_attention_forward_lse,
+                                                             flash_attention)
+from oracle.attention import attention_grads, attention_reference, flash_backward_tiled
+from oracle.inputs import make_config_inputs
+from tests.gates import assert_gate, assert_grad_parity
+
+pytestmark = pytest.mark.gpu
+
+GRADCHECK_SHAPES = [(1, 1, 4, 8), (1, 2, 9, 16)]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,N,D", GRADCHECK_SHAPES)
+def test_gradcheck(gpu, B, H, N, D, causal):
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(B, H, N, D, device=gpu, dtype=torch.float32, requires_grad=True) for _ in range(3))
+    assert torch.autograd.gradcheck(lambda a, b, c: flash_attention(a, b, c, causal=causal), (q, k, v),
+                                    eps=1e-3, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,N,D", [(1, 1, 17, 32), (2, 2, 64, 64), (1, 4, 130, 64), (2, 8, 256, 128)])
+def test_matches_oracle_autograd(gpu, B, H, N, D, dtype, causal):
+    print(f"case bwd {B}x{H}x{N}x{D} {dtype} causal={causal}", flush=True)
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(B, H, N, D, device=gpu, dtype=dtype, requires_grad=True) for _ in range(3))
+    do = torch.randn(B, H, N, D, device=gpu, dtype=dtype)
+    out = flash_attention(q, k, v, causal=causal)
+    out.backward(do)
+    dq_r, dk_r, dv_r = attention_grads(q.detach().cpu(), k.detach().cpu(), v.detach().cpu(), do.cpu(), causal)
+    tol = 1e-3 if dtype == torch.float32 else 3e-2
+    for name, got, ref in (("dq", q.grad, dq_r), ("dk", k.grad, dk_r), ("dv", v.grad, dv_r)):
+        assert got.dtype == dtype
+        torch.testing.assert_close(got.cpu().double(), ref, atol=tol, rtol=tol, msg=lambda m: f"{name}: {m}")
+        if dtype != torch.float32:
+            assert_gate(got.cpu(), ref, f"{name} {dtype}")
+
+
+def test_forward_matches_forward_only_kernel(gpu):
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(2, 4, 130, 64, device=gpu, dtype=torch.float32) for _ in range(3))
+    torch.testing.assert_close(flash_attention(q, k, v, causal=True),
+                               flash_attention_forward(q, k, v, causal=True), atol=1e-3, rtol=1e-3)
+
+
+def test_backward_deterministic_and_strided_do(gpu):
+    """No atomics: two backward passes are bitwise equal; a non-contiguous dO
+    gives the same gradients as its contiguous copy."""
+    torch.manual_seed(1)
+    q, k, v = (torch.randn(2, 4, 300, 128, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    o, L = _flash_attention_forward_lse(q, k, v, True)
+    do_t = torch.randn(2, 300, 4, 128, device=gpu, dtype=torch.bfloat16).transpose(1, 2)
+    g1 = _flash_attention_backward(do_t, q, k, v, o, L, True)
+    g2 = _flash_attention_backward(do_t.contiguous(), q, k, v, o, L, True)
+    g3 = _flash_attention_backward(do_t, q, k, v, o, L, True)
+    for a, b, c in zip(g1, g2, g3):
+        assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.parametrize("D", [12, 96])
+def test_backward_padded_head_dim(gpu, D):
+    torch.manual_seed(2)
+    q, k, v = (torch.randn(1, 2, 90, D, device=gpu, dtype=torch.bfloat16, requires_grad=True) for _ in range(3))
+    do = torch.randn(1, 2, 90, D, device=gpu, dtype=torch.bfloat16)
+    flash_attention(q, k, v, causal=True).backward(do)
+    refs = attention_grads(q.detach().cpu(), k.detach().cpu(), v.detach().cpu(), do.cpu(), True)
+    for name, got, ref in zip(("dq", "dk", "dv"), (q.grad, k.grad, v.grad), refs):
+        assert_gate(got.cpu(), ref, f"D={D} {name}")
+
+
+def _grads_gpu_fp32(q, k, v, do, causal):
+    return attention_grads(q, k, v, do, causal, dtype=torch.float32)
+
+
+@pytest.mark.parametrize("cfg", [3, 4])
+def test_config_backward_full_size(gpu, cfg):
+    """BASELINE gate on dQ/dK/dV at the full config size, checked on a few
+    (batch, head) slices with the oracle's fp32 autograd on the GPU."""
+    print(f"case config {cfg} backward full size", flush=True)
+    inp = make_config_inputs(cfg, device=gpu)
+    q, k, v, do, causal = inp["q"], inp["k"], inp["v"], inp["do"], inp["causal"]
+    o, L = _flash_attention_forward_lse(q, k, v, causal)
+    dq, dk, dv = _flash_attention_backward(do, q, k, v, o, L, causal)
+    slices = [(0, 0), (q.shape[0] - 1, q.shape[1] - 1)] if cfg == 3 else [(0, 3), (0, 12)]
+    for b, h in slices:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        exact = _grads_gpu_fp32(q[sl], k[sl], v[sl], do[sl], causal)
+        o_ref, lse_ref = attention_reference(q[sl], k[sl], v[sl], causal, dtype=torch.float32)
+        assert_gate(o[sl], o_ref, f"config {cfg} (b={b},h={h}) o")
+        # the reference's own algorithm: stored o in the input dtype, fp32 L,
+        # P and dS rounded to the input dtype before their products
+        ref_alg = flash_backward_tiled(q[sl], k[sl], v[sl], o_ref.to(q.dtype), lse_ref, do[sl], causal,
+                                       block_n=256, op_dtype=q.dtype)
+        for name, got, ex, ra in zip(("dq", "dk", "dv"), (dq[sl], dk[sl], dv[sl]), exact, ref_alg):
+            assert_grad_parity(got, ex, ra, f"config {cfg} (b={b},h={h}) {name}")

@@ -1,0 +1,188 @@
+"""GPU parity of the forward kernels against the oracle (oracle/attention.py).
+
+Mirrors the reference's forward tests (kernels/tests/test_flash_attention.py:
+shapes :24-31, dtypes and tolerances :40-61, non-contiguous input :65-77)
+with the oracle in place of SDPA, adds fp16, logsumexp, the BASELINE gate at
+the full config sizes, head dims that need padding, graph capture and a
+side stream.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from lightserve_amd.kernels.flash_attention import flash_attention_forward
+from oracle.attention import attention_reference
+from oracle.inputs import make_config_inputs
+from tests.gates import assert_gate, assert_lse
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1, 1, 8), (1, 1, 17, 32), (2, 2, 64, 64), (1, 4, 130, 64), (2, 8, 256, 128), (1, 2, 100, 96)]
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def _oracle_cpu(q, k, v, causal, sm_scale=None):
+    return attention_reference(q.cpu(), k.cpu(), v.cpu(), causal, sm_scale)
+
+
+def _oracle_gpu_chunked(q, k, v, causal, heads_per_chunk=8):
+    """fp32 oracle on the GPU, a few heads at a time (large configs)."""
+    B, H = q.shape[:2]
+    o = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+    lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+    for b in range(B):
+        for h0 in range(0, H, heads_per_chunk):
+            sl = (b, slice(h0, h0 + heads_per_chunk))
+            ob, lb = attention_reference(q[sl], k[sl], v[sl], causal, dtype=torch.float32)
+            o[sl], lse[sl] = ob, lb
+    return o, lse
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,H,N,D", SHAPES)
+def test_matches_oracle_reference_shapes(gpu, B, H, N, D, dtype, causal):
+    print(f"case fwd {B}x{H}x{N}x{D} {dtype} causal={causal}", flush=True)
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(B, H, N, D, device=gpu, dtype=dtype) for _ in range(3))
+    o, lse = flash_attention_forward(q, k, v, causal=causal, return_lse=True)
+    o_ref, lse_ref = _oracle_cpu(q, k, v, causal)
+    if dtype == torch.float32:
+        torch.testing.assert_close(o.cpu().double(), o_ref, atol=1e-3, rtol=1e-3)
+    else:
+        torch.testing.assert_close(o.cpu().double(), o_ref, atol=2e-2, rtol=2e-2)
+        assert_gate(o.cpu(), o_ref, f"o {dtype}")
+    assert_lse(lse.cpu(), lse_ref, "lse")
+    o_only = flash_attention_forward(q, k, v, causal=causal)
+    assert torch.equal(o_only, o), "return_lse must not change the output"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_matches_oracle_non_contiguous(gpu, dtype):
+    """The reference's transposed-heads view (kernels/tests/test_flash_attention.py:65-77)."""
+    torch.manual_seed(0)
+    q = torch.randn(1, 64, 4, 32, device=gpu, dtype=dtype).transpose(1, 2)
+    k = torch.randn(1, 4, 64, 32, device=gpu, dtype=dtype)
+    v = torch.randn(1, 4, 64, 32, device=gpu, dtype=dtype)
+    o = flash_attention_forward(q, k, v)
+    assert o.stride() == q.stride(), "o must keep q's strides (empty_like)"
+    o_ref, _ = _oracle_cpu(q, k, v, False)
+    tol = 1e-3 if dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(o.cpu().double(), o_ref, atol=tol, rtol=tol)
+
+
+def test_model_layout_bf16(gpu):
+    """q/k/v as the model passes them: [B, H, N, D] views over [B, N, H, D]
+    memory (model/minimal_llama.py:216-221), read in place."""
+    torch.manual_seed(1)
+    B, N, H, D = 2, 300, 8, 128
+    q, k, v = (torch.randn(B, N, H, D, device=gpu, dtype=torch.bfloat16).transpose(1, 2) for _ in range(3))
+    o, lse = flash_attention_forward(q, k, v, causal=True, return_lse=True)
+    o_ref, lse_ref = _oracle_cpu(q, k, v, True)
+    assert_gate(o.cpu(), o_ref, "model layout o")
+    assert_lse(lse.cpu(), lse_ref, "model layout")
+
+
+@pytest.mark.parametrize("D", [12, 40, 72])
+def test_padded_head_dim_bf16(gpu, D):
+    """Head dims that are not multiples of 8 go through a zero-padded copy."""
+    torch.manual_seed(2)
+    q, k, v = (torch.randn(2, 3, 77, D, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    o, lse = flash_attention_forward(q, k, v, causal=True, return_lse=True)
+    o_ref, lse_ref = _oracle_cpu(q, k, v, True)
+    assert_gate(o.cpu(), o_ref, f"D={D} o")
+    assert_lse(lse.cpu(), lse_ref, f"D={D}")
+
+
+def test_sm_scale_argument(gpu):
+    torch.manual_seed(3)
+    q, k, v = (torch.randn(1, 2, 200, 64, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    o, lse = flash_attention_forward(q, k, v, causal=False, sm_scale=0.3, return_lse=True)
+    o_ref, lse_ref = _oracle_cpu(q, k, v, False, 0.3)
+    assert_gate(o.cpu(), o_ref, "sm_scale o")
+    assert_lse(lse.cpu(), lse_ref, "sm_scale")
+
+
+def test_config1_against_golden(gpu):
+    """Config 1 (fp32 causal 1x4x256x64, seed 0) against the pure-Python loop
+    fixture of tests/golden."""
+    golden = np.load(os.path.join(os.path.dirname(__file__), "golden", "attention_golden.npz"))
+    inp = make_config_inputs(1, device=gpu)
+    o, lse = flash_attention_forward(inp["q"], inp["k"], inp["v"], causal=True, return_lse=True)
+    np.testing.assert_allclose(o[0, :, ::8, :].cpu().double().numpy(), golden["cfg1/o_rows"], atol=1e-4)
+    np.testing.assert_allclose(lse[0].cpu().double().numpy(), golden["cfg1/lse"], atol=1e-4)
+
+
+@pytest.mark.parametrize("cfg", [2, 3, 4])
+def test_config_forward_full_size(gpu, cfg):
+    """BASELINE gate at the full config size (oracle in fp32 on the GPU;
+    config 4 checks 4 of its 16 heads to bound the oracle's time)."""
+    print(f"case config {cfg} forward full size", flush=True)
+    inp = make_config_inputs(cfg, device=gpu)
+    q, k, v, causal = inp["q"], inp["k"], inp["v"], inp["causal"]
+    o, lse = flash_attention_forward(q, k, v, causal=causal, return_lse=True)
+    if cfg == 4:
+        heads = [0, 5, 10, 15]
+        o, lse = o[:, heads], lse[:, heads]
+        q, k, v = q[:, heads], k[:, heads], v[:, heads]
+        o_ref, lse_ref = _oracle_gpu_chunked(q, k, v, causal, heads_per_chunk=1)
+    else:
+        o_ref, lse_ref = _oracle_gpu_chunked(q, k, v, causal)
+    assert_gate(o, o_ref, f"config {cfg} o")
+    assert_lse(lse, lse_ref, f"config {cfg}")
+
+
+def test_zero_query_property_full_size(gpu):
+    """Size-independent closed form at config 3's shape: with q = 0 every
+    visible key scores 0, so o_i is the mean of v_0..v_i and L_i = ln(i+1)."""
+    inp = make_config_inputs(3, device=gpu)
+    v = inp["v"][:, :4]
+    q = torch.zeros_like(v)
+    o, lse = flash_attention_forward(q, inp["k"][:, :4], v, causal=True, return_lse=True)
+    n = v.shape[2]
+    idx = torch.arange(1, n + 1, device=gpu, dtype=torch.float64)
+    mean = v.double().cumsum(2) / idx.view(1, 1, n, 1)
+    assert_gate(o, mean, "q=0 prefix mean")
+    torch.testing.assert_close(lse.double(), torch.log(idx).expand_as(lse), atol=1e-4, rtol=0)
+
+
+def test_edge_sizes(gpu):
+    torch.manual_seed(4)
+    for (B, H, N, D) in [(1, 1, 1, 128), (3, 1, 129, 64), (1, 2, 255, 32), (1, 1, 513, 128)]:
+        q, k, v = (torch.randn(B, H, N, D, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+        for causal in (False, True):
+            o, lse = flash_attention_forward(q, k, v, causal=causal, return_lse=True)
+            o_ref, lse_ref = _oracle_cpu(q, k, v, causal)
+            assert_gate(o.cpu(), o_ref, f"edge {B}x{H}x{N}x{D} causal={causal}")
+            assert_lse(lse.cpu(), lse_ref, "edge")
+    empty = torch.empty(1, 2, 0, 64, device=gpu, dtype=torch.bfloat16)
+    assert flash_attention_forward(empty, empty, empty).shape == empty.shape
+
+
+def test_graph_capture_and_side_stream(gpu):
+    """The call captures into a HIP graph (no host sync, no allocation by the
+    library); every replay matches the eager result, with eager work and
+    synchronisation between replays."""
+    torch.manual_seed(5)
+    q, k, v = (torch.randn(2, 4, 333, 128, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    eager = flash_attention_forward(q, k, v, causal=True)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        o_side = flash_attention_forward(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_side, eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        flash_attention_forward(q, k, v, causal=True)  # warm-up on the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=side):
+            out = flash_attention_forward(q, k, v, causal=True)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs"
+        _ = (q.float() * 2).sum().item()  # unrelated eager work between replays

@@ -1,0 +1,222 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+Checks, per oracle function:
+  attention_reference  vs pure-Python loop fixtures (tests/golden), closed-form
+                       invariants, torch SDPA (float64);
+  attention_grads      float64 gradcheck;
+  flash_forward_tiled  (restated reference tile loop) vs attention_reference;
+  flash_backward_tiled (restated reference backward) vs attention_grads;
+  varlen_reference     vs pure-Python loops with GQA;
+and planted mistakes in copies of the oracle must fail these checks.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle.attention import (attention_grads, attention_reference, causal_mask, flash_backward_tiled,
+                              flash_forward_tiled, naive_attention, varlen_reference)
+from oracle.inputs import CONFIGS, make_config_inputs, make_varlen_inputs, varlen_fwd_flops
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "attention_golden.npz")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN)  # allow_pickle stays False
+
+
+def _tiny_names(golden):
+    return sorted({k.split("/")[0] for k in golden.files if not k.startswith("cfg1")})
+
+
+def test_golden_tiny_cases(golden):
+    names = _tiny_names(golden)
+    assert len(names) == 8
+    for name in names:
+        H, Hkv, nq, nk, d, causal, scale = golden[f"{name}/meta"].tolist()
+        scale = None if scale < 0 else scale
+        q, k, v = (torch.from_numpy(golden[f"{name}/{t}"]) for t in "qkv")
+        group = int(H) // int(Hkv)
+        k_rep = k.repeat_interleave(group, dim=0)
+        v_rep = v.repeat_interleave(group, dim=0)
+        o, lse = attention_reference(q, k_rep, v_rep, bool(causal), scale)
+        np.testing.assert_allclose(o.numpy(), golden[f"{name}/o"], atol=1e-12, rtol=1e-12, err_msg=name)
+        np.testing.assert_allclose(lse.numpy(), golden[f"{name}/lse"], atol=1e-12, rtol=1e-12, err_msg=name)
+
+
+def test_golden_config1(golden):
+    """Config 1 (the CPU plumbing case): inputs regenerate bit-identically from
+    the seed, and the float64 oracle matches the pure-Python loop outputs."""
+    import hashlib
+    inp = make_config_inputs(1)
+    for i, n in enumerate("qkv"):
+        assert hashlib.sha256(inp[n].contiguous().numpy().tobytes()).hexdigest() == golden["cfg1/sha256"][i]
+    o, lse = attention_reference(inp["q"], inp["k"], inp["v"], causal=True)
+    np.testing.assert_allclose(lse[0].numpy(), golden["cfg1/lse"], atol=1e-10)
+    np.testing.assert_allclose(o[0, :, ::8, :].numpy(), golden["cfg1/o_rows"], atol=1e-10)
+    np.testing.assert_allclose([o.sum().item(), (o * o).sum().item()], golden["cfg1/o_sum"], rtol=1e-10)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("nq,nk", [(7, 7), (5, 11)])
+def test_invariant_zero_query(causal, nq, nk):
+    """q = 0: every visible key scores 0, so o is the mean of the visible v rows
+    and lse = ln(#visible keys)."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.zeros(2, nq, 16, dtype=torch.float64)
+    k = torch.randn(2, nk, 16, generator=g, dtype=torch.float64)
+    v = torch.randn(2, nk, 16, generator=g, dtype=torch.float64)
+    o, lse = attention_reference(q, k, v, causal)
+    for i in range(nq):
+        n_vis = min(nk, i + 1 + nk - nq) if causal else nk
+        torch.testing.assert_close(o[:, i], v[:, :n_vis].mean(1), atol=1e-12, rtol=0)
+        torch.testing.assert_close(lse[:, i], torch.full((2,), math.log(n_vis), dtype=torch.float64))
+
+
+def test_invariant_causal_first_row():
+    """Causal, Nq == Nk: row 0 sees only key 0, so o_0 = v_0 and L_0 = s*q_0.k_0."""
+    g = torch.Generator().manual_seed(6)
+    q, k, v = (torch.randn(3, 9, 8, generator=g, dtype=torch.float64) for _ in range(3))
+    o, lse = attention_reference(q, k, v, causal=True, sm_scale=0.3)
+    torch.testing.assert_close(o[:, 0], v[:, 0], atol=1e-14, rtol=0)
+    torch.testing.assert_close(lse[:, 0], 0.3 * (q[:, 0] * k[:, 0]).sum(-1), atol=1e-14, rtol=0)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 17, 32), (2, 2, 64, 64), (1, 4, 130, 64), (1, 2, 100, 96)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_matches_sdpa_float64(shape, causal):
+    """Library routine: torch SDPA (the reference's own oracle) in float64."""
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(*shape, generator=g, dtype=torch.float64) for _ in range(3))
+    o, _ = attention_reference(q, k, v, causal)
+    torch.testing.assert_close(o, F.scaled_dot_product_attention(q, k, v, is_causal=causal), atol=1e-12, rtol=1e-12)
+
+
+def test_lse_is_logsumexp_of_masked_scores():
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(2, 6, 10, 8, generator=g, dtype=torch.float64) for _ in range(3))
+    _, lse = attention_reference(q, k, v, True, 0.5)
+    s = (q @ k.transpose(-1, -2)) * 0.5
+    expect = torch.stack([torch.logsumexp(s[..., i, : i + 1], -1) for i in range(10)], -1)
+    torch.testing.assert_close(lse, expect, atol=1e-13, rtol=0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_grads_gradcheck(causal):
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(1, 2, 6, 4, generator=g, dtype=torch.float64, requires_grad=True) for _ in range(3))
+    assert torch.autograd.gradcheck(lambda a, b, c: attention_reference(a, b, c, causal)[0], (q, k, v))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("nq,nk", [(130, 130), (70, 150)])
+def test_tiled_forward_restatement(causal, nq, nk):
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(2, 3, nq, 64, generator=g)
+    k = torch.randn(2, 3, nk, 64, generator=g)
+    v = torch.randn(2, 3, nk, 64, generator=g)
+    o_ref, l_ref = attention_reference(q, k, v, causal)
+    o, l = flash_forward_tiled(q, k, v, causal, block_n=32)
+    torch.testing.assert_close(o.double(), o_ref, atol=2e-6, rtol=0)
+    torch.testing.assert_close(l.double(), l_ref, atol=2e-6, rtol=0)
+    # p rounded to bf16 before PV (the reference's p.to(v.dtype)) stays inside the BASELINE gate
+    ob, _ = flash_forward_tiled(q, k, v, causal, block_n=32, p_dtype=torch.bfloat16)
+    err = (ob.double() - o_ref).abs()
+    assert err.max() < 2e-2 and err.mean() < 2e-3
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_tiled_backward_restatement(causal):
+    g = torch.Generator().manual_seed(10)
+    q, k, v, do = (torch.randn(2, 2, 100, 32, generator=g) for _ in range(4))
+    o, lse = attention_reference(q, k, v, causal)
+    dq_r, dk_r, dv_r = attention_grads(q, k, v, do, causal)
+    dq, dk, dv = flash_backward_tiled(q, k, v, o.float(), lse.float(), do, causal, block_n=32)
+    for got, ref in ((dq, dq_r), (dk, dk_r), (dv, dv_r)):
+        torch.testing.assert_close(got.double(), ref, atol=2e-5, rtol=0)
+
+
+def test_varlen_matches_loops():
+    g = torch.Generator().manual_seed(11)
+    cu_q = torch.tensor([0, 3, 5, 9], dtype=torch.int32)
+    cu_k = torch.tensor([0, 7, 9, 18], dtype=torch.int32)
+    q = torch.randn(9, 4, 8, generator=g, dtype=torch.float64)
+    k = torch.randn(18, 2, 8, generator=g, dtype=torch.float64)
+    v = torch.randn(18, 2, 8, generator=g, dtype=torch.float64)
+    o, lse = varlen_reference(q, k, v, cu_q, cu_k, causal=True)
+    for b in range(3):
+        qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        on, ln = naive_attention(q[qs:qe].transpose(0, 1).tolist(), k[ks:ke].transpose(0, 1).tolist(),
+                                 v[ks:ke].transpose(0, 1).tolist(), True, None, group=2)
+        np.testing.assert_allclose(o[qs:qe].transpose(0, 1).numpy(), np.array(on), atol=1e-12)
+        np.testing.assert_allclose(lse[:, qs:qe].numpy(), np.array(ln), atol=1e-12)
+
+
+def test_causal_mask_bottom_right():
+    m = causal_mask(2, 4)
+    assert m.tolist() == [[True, True, True, False], [True, True, True, True]]
+    assert torch.equal(causal_mask(5, 5), torch.ones(5, 5, dtype=torch.bool).tril())
+
+
+def test_config_recipes():
+    a = make_config_inputs(3, shape_override=(1, 2, 64, 32))
+    b = make_config_inputs(3, shape_override=(1, 2, 64, 32))
+    assert all(torch.equal(a[n], b[n]) for n in ("q", "k", "v", "do"))
+    assert a["q"].dtype == torch.bfloat16 and a["q"].float().abs().max() < 4
+    c = make_config_inputs(4, shape_override=(1, 2, 400, 16))
+    idx = c["scaled_rows"]
+    assert idx.numel() == 4
+    # the scaled rows carry ~8x the norm of the others
+    norms = c["k"].float().norm(dim=-1)[0, 0]
+    mask = torch.zeros(400, dtype=torch.bool)
+    mask[idx] = True
+    assert norms[mask].mean() > 5 * norms[~mask].mean()
+    vl = make_varlen_inputs(batch=3, chunk=16, prefix=(10, 20), heads=(4, 2), D=8)
+    assert vl["q"].shape == (48, 4, 8) and vl["cu_seqlens_k"][-1] == vl["k"].shape[0]
+    assert all(10 <= int(p) <= 20 for p in vl["prefix"])
+    assert CONFIGS[5]["Hq"] % CONFIGS[5]["Hkv"] == 0
+    # exact varlen FLOPs: brute force pair count
+    cu_q, cu_k = vl["cu_seqlens_q"], vl["cu_seqlens_k"]
+    pairs = sum(int(causal_mask(int(cu_q[b + 1] - cu_q[b]), int(cu_k[b + 1] - cu_k[b])).sum()) for b in range(3))
+    assert varlen_fwd_flops(cu_q, cu_k, 4, 8) == 4 * 8 * 4 * pairs
+
+
+# --- planted mistakes: each broken copy of the oracle must fail a check above ---
+
+def _broken_scale_twice(q, k, v, causal=False, sm_scale=None):
+    d = q.shape[-1]
+    s = (1.0 / math.sqrt(d)) if sm_scale is None else sm_scale
+    return attention_reference(q, k, v, causal, s * s)
+
+
+def _broken_transposed_v(q, k, v, causal=False, sm_scale=None):
+    o, lse = attention_reference(q, k, v.transpose(-1, -2).contiguous().transpose(-1, -2).flip(-2), causal, sm_scale)
+    return o, lse
+
+
+def _broken_top_left_mask(q, k, v, causal=False, sm_scale=None):
+    q64, k64, v64 = q.double(), k.double(), v.double()
+    s = (q64 @ k64.transpose(-1, -2)) / math.sqrt(q.shape[-1]) if sm_scale is None else (q64 @ k64.transpose(-1, -2)) * sm_scale
+    if causal:
+        nq, nk = s.shape[-2:]
+        s = s.masked_fill(torch.ones(nq, nk, dtype=torch.bool).triu(1), float("-inf"))
+    lse = torch.logsumexp(s, -1)
+    return torch.exp(s - lse.unsqueeze(-1)) @ v64, lse
+
+
+@pytest.mark.parametrize("broken", [_broken_scale_twice, _broken_transposed_v, _broken_top_left_mask])
+def test_planted_mistakes_are_caught(golden, broken):
+    caught = 0
+    for name in _tiny_names(golden):
+        H, Hkv, nq, nk, d, causal, scale = golden[f"{name}/meta"].tolist()
+        q, k, v = (torch.from_numpy(golden[f"{name}/{t}"]) for t in "qkv")
+        group = int(H) // int(Hkv)
+        o, _ = broken(q, k.repeat_interleave(group, 0), v.repeat_interleave(group, 0), bool(causal),
+                      None if scale < 0 else scale)
+        if not np.allclose(o.numpy(), golden[f"{name}/o"], atol=1e-9):
+            caught += 1
+    assert caught > 0, f"{broken.__name__} passed every golden case"
