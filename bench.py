@@ -1,0 +1,273 @@
+"""Benchmark of the gfx950 FlashAttention hot path (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3] [--no-cpu-baseline]
+
+A step is one pass of the training hot path over one batch of synthetic
+input: forward with logsumexp, then backward (dQ, dK, dV), on BASELINE
+config 3 (causal bf16, B=4, H=32, N=4096, D=128, q/k/v ~ N(0,1)*0.5, dO ~
+N(0,1), seed 2) by default; --config 2/4/5 time the other configurations
+(forward only for 2 and 5). Inputs are resident in HBM before the timed
+region. FLOPs follow the reference's convention
+(kernels/benchmark_flash_attention.py:55-64,
+kernels/benchmark_flash_attention_backward.py:65-68): F_fwd = 4*B*H*N^2*D,
+halved when causal; F_bwd = 2.5*F_fwd; a fwd+bwd step counts 3.5*F_fwd.
+
+Timing: W untimed warm-up steps; then K steps bracketed by
+torch.cuda.synchronize() on both sides; HIP events on the launch stream
+around each phase give the per-phase (per-launch) kernel time used for the
+forward TFLOP/s and the roofline. Correctness is re-checked against the
+oracle on two (batch, head) slices before timing, as the reference does
+(kernels/benchmark_flash_attention.py:104-106).
+
+The CPU baseline is the reference's test oracle (F.scaled_dot_product_attention
+in fp32 with autograd, kernels/tests/test_flash_attention_backward.py:86)
+on a bounded sample of heads of the same workload, run on this host's cores
+and scaled linearly to the full job.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16/fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+HBM_PEAK_GBS = 8000.0
+METRIC = "attention TFLOP/s fwd & fwd+bwd, % of MI355X bf16 MFMA peak, 1 GPU"
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=2, help="heads in the CPU-baseline sample")
+    return ap.parse_args()
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (profiles/hbm_traffic.txt: `kernel workload bytes_per_launch`), or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        parts = line.split()
+        if len(parts) >= 3 and not line.startswith("#") and parts[0] == kernel and parts[1] == workload:
+            return float(parts[2])
+    return None
+
+
+def check_parity(cfg, inp, outs):
+    """Oracle check of two (batch, head) slices (fp32 oracle on the GPU)."""
+    import torch
+    from oracle.attention import attention_grads, attention_reference
+    q, k, v, causal = inp["q"], inp["k"], inp["v"], inp["causal"]
+    worst = {}
+    B, H = q.shape[:2]
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        o_ref, lse_ref = attention_reference(q[sl], k[sl], v[sl], causal, dtype=torch.float32)
+        pairs = [("o", outs["o"][sl], o_ref), ("lse", outs["lse"][sl], lse_ref)]
+        if "dq" in outs:
+            g = attention_grads(q[sl], k[sl], v[sl], inp["do"][sl], causal, dtype=torch.float32)
+            pairs += [("dq", outs["dq"][sl], g[0]), ("dk", outs["dk"][sl], g[1]), ("dv", outs["dv"][sl], g[2])]
+        for name, got, ref in pairs:
+            err = (got.double() - ref.double()).abs()
+            mx, mn = err.max().item(), err.mean().item()
+            prev = worst.get(name, (0.0, 0.0))
+            worst[name] = (max(prev[0], mx), max(prev[1], mn))
+    res = {n: {"max_abs": float(f"{m:.3e}"), "mean_abs": float(f"{a:.3e}")} for n, (m, a) in worst.items()}
+    ok = all(res[n]["max_abs"] <= 2e-2 and res[n]["mean_abs"] <= 2e-3 for n in ("o",) if n in res)
+    ok = ok and res["lse"]["max_abs"] <= 1e-3
+    return ok, res
+
+
+def cpu_baseline(cfg, inp, n_heads, flops_full, step_kind):
+    """Times F.scaled_dot_product_attention (fp32, CPU) on n_heads heads of the
+    workload (1 warm-up, median of 3) and scales to the full job."""
+    import torch
+    import torch.nn.functional as F
+    q, k, v = (inp[n][:1, :n_heads].float().cpu() for n in ("q", "k", "v"))
+    do = inp["do"][:1, :n_heads].float().cpu() if "do" in inp else None
+    causal = inp["causal"]
+
+    def run():
+        if step_kind == "fwd+bwd":
+            qq, kk, vv = (t.clone().requires_grad_() for t in (q, k, v))
+            F.scaled_dot_product_attention(qq, kk, vv, is_causal=causal).backward(do)
+        else:
+            F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    total_heads = inp["q"].shape[0] * inp["q"].shape[1]
+    full_s = t * total_heads / n_heads
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(flops_full / full_s / 1e12, 4), "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"F.scaled_dot_product_attention fp32 {step_kind} on {n_heads} of {total_heads} (b,h) heads "
+                   f"(1 warm-up, median of 3: {t:.2f} s), scaled linearly; os.cpu_count()={os.cpu_count()}; "
+                   f"{cpu_model}"),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from lightserve_amd import _lib
+    from lightserve_amd.kernels.flash_attention_backward import (_flash_attention_backward,
+                                                                 _flash_attention_forward_lse)
+    from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen_forward
+    from oracle.inputs import CONFIGS, bwd_flops, fwd_flops, make_config_inputs, make_varlen_inputs, varlen_fwd_flops
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    cfg = CONFIGS[args.config]
+    stream = torch.cuda.current_stream(dev)
+
+    if args.config == 5:
+        inp = make_varlen_inputs(device=dev)
+        q, k, v = inp["q"], inp["k"], inp["v"]
+        f_fwd = varlen_fwd_flops(inp["cu_seqlens_q"].cpu(), inp["cu_seqlens_k"].cpu(), cfg["Hq"], cfg["D"])
+        f_step = f_fwd
+        step_kind = "fwd"
+
+        def fwd():
+            return flash_attention_varlen_forward(q, k, v, inp["cu_seqlens_q"], inp["cu_seqlens_k"],
+                                                  inp["max_seqlen_q"], inp["max_seqlen_k"])
+        bwd = None
+        workload = (f"config5: varlen GQA chunked prefill bf16 B=8 Hq=32 Hkv=8 D=128 chunk=512 "
+                    f"prefix={inp['prefix'].tolist()}")
+    else:
+        inp = make_config_inputs(args.config, device=dev)
+        q, k, v, causal = inp["q"], inp["k"], inp["v"], inp["causal"]
+        B, H, N, D = q.shape
+        f_fwd = fwd_flops(B, H, N, D, causal)
+        step_kind = "fwd+bwd" if cfg["backward"] else "fwd"
+        f_step = f_fwd + (bwd_flops(B, H, N, D, causal) if cfg["backward"] else 0)
+
+        def fwd():
+            return _flash_attention_forward_lse(q, k, v, causal)
+
+        if cfg["backward"]:
+            do = inp["do"]
+
+            def bwd(o, lse):
+                return _flash_attention_backward(do, q, k, v, o, lse, causal)
+        else:
+            bwd = None
+        workload = (f"config{args.config}: {'causal' if causal else 'non-causal'} {str(q.dtype)[6:]} {step_kind} "
+                    f"B={B} H={H} N={N} D={D}")
+
+    # correctness re-check before timing
+    o, lse = fwd()
+    outs = {"o": o, "lse": lse}
+    if bwd is not None:
+        outs["dq"], outs["dk"], outs["dv"] = bwd(o, lse)
+    torch.cuda.synchronize()
+    if args.config == 5:
+        from oracle.attention import attention_reference
+        cq, ck = inp["cu_seqlens_q"].tolist(), inp["cu_seqlens_k"].tolist()
+        qb = q[cq[0]:cq[1]].transpose(0, 1)
+        kb = k[ck[0]:ck[1]].transpose(0, 1).repeat_interleave(4, 0)
+        vb = v[ck[0]:ck[1]].transpose(0, 1).repeat_interleave(4, 0)
+        o_ref, _ = attention_reference(qb, kb, vb, True, dtype=torch.float32)
+        err = (o[cq[0]:cq[1]].transpose(0, 1).double() - o_ref.double()).abs()
+        parity = {"o": {"max_abs": float(f"{err.max().item():.3e}"), "mean_abs": float(f"{err.mean().item():.3e}")}}
+        parity_ok = parity["o"]["max_abs"] <= 2e-2 and parity["o"]["mean_abs"] <= 2e-3
+    else:
+        parity_ok, parity = check_parity(cfg, inp, outs)
+    del outs
+
+    def step():
+        o, lse = fwd()
+        if bwd is not None:
+            bwd(o, lse)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        e0, e1, e2 = ev[i]
+        e0.record(stream)
+        o, lse = fwd()
+        e1.record(stream)
+        if bwd is not None:
+            bwd(o, lse)
+        e2.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    fwd_ms = [a.elapsed_time(b) for a, b, _ in ev]
+    bwd_ms = [b.elapsed_time(c) for _, b, c in ev]
+    step_ms = [a.elapsed_time(c) for a, _, c in ev]
+    ms_per_step = sum(step_ms) / len(step_ms)
+    value = f_step / (ms_per_step * 1e-3) / 1e12
+    fwd_avg = sum(fwd_ms) / len(fwd_ms)
+    fwd_tflops = f_fwd / (fwd_avg * 1e-3) / 1e12
+
+    wl_key = f"config{args.config}"
+    traffic = measured_traffic("fa_fwd_kernel", wl_key)
+    roofline = {"kernel": "fa_fwd_kernel", "bound": "mfma", "achieved": round(fwd_tflops, 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(fwd_tflops / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic,
+                "flops_per_launch": f_fwd, "avg_launch_ms": round(fwd_avg, 5)}
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if q.dtype == torch.bfloat16 else ("fp16" if q.dtype == torch.float16 else "fp32"),
+        "data": f"synthetic, seeded (seed {cfg['seed']}), inputs resident in HBM",
+        "config": {"workload": workload, "step": step_kind, "flops_per_step": f_step},
+        "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "fwd": {"tflops": round(fwd_tflops, 2), "ms": round(fwd_avg, 5),
+                "pct_of_peak": round(100 * fwd_tflops / PEAK_BF16_TFLOPS, 2)},
+        "wall_s_timed": round(wall, 4),
+        "parity": {"ok": parity_ok, **parity},
+        "roofline": roofline,
+    }
+    if bwd is not None:
+        bwd_avg = sum(bwd_ms) / len(bwd_ms)
+        fb = bwd_flops(*q.shape, inp["causal"])
+        result["bwd"] = {"tflops": round(fb / (bwd_avg * 1e-3) / 1e12, 2), "ms": round(bwd_avg, 5),
+                         "pct_of_peak": round(100 * fb / (bwd_avg * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                         "kernels": "fa_bwd_dq_kernel + fa_bwd_dkdv_kernel"}
+        result["fwd_bwd"] = {"tflops": round(value, 2), "ms": round(ms_per_step, 5),
+                             "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2)}
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, inp, args.cpu_heads, f_step, step_kind) if args.config != 5 else None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
