@@ -115,7 +115,11 @@ int lsfa_fwd(const lsfa_fwd_args* a, void* stream) {
   p.cu_k = a->cu_seqlens_k;
   p.B = a->batch; p.Hq = a->heads_q; p.Hkv = a->heads_kv;
   p.Nq = a->seqlen_q; p.Nk = a->seqlen_k; p.D = a->head_dim;
-  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  // The MFMA kernels keep the exponent scale positive (a negative scale is
+  // folded into q) and nonzero (a zero scale becomes 1e-30: every score is 0
+  // to within fp32 rounding either way).
+  p.scale_log2 = fmaxf(fabsf(a->sm_scale) * 1.4426950408889634f, 1e-30f);
+  p.neg_q = a->sm_scale < 0.f;
   const bool varlen = a->cu_seqlens_q != nullptr;
   const int dp = padded_dim(a->head_dim);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);

@@ -44,7 +44,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) T smem_raw[4 * TILE];
   LDS_AS T* smem = (LDS_AS T*)smem_raw;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
   int bh, qt;
   map_tile(p.num_tiles, gridDim.x, bh, qt, CAUSAL);
@@ -226,7 +227,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   __shared__ __attribute__((aligned(16))) char smem_raw[2 * STAGE];
   LDS_AS char* smem = (LDS_AS char*)smem_raw;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
   int bh, kt;
   map_tile(p.num_tiles, gridDim.x, bh, kt, false);

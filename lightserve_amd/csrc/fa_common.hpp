@@ -71,6 +71,25 @@ __device__ __forceinline__ typename VecT<T>::x8 pack8(const f32x16& c, int base)
   return r;
 }
 
+// acc + sum of the 8 elements of a bf16/f16 operand (four v_dot2 with 1.0).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_ones(bf16x2 v, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
+}
+__device__ __forceinline__ float dot2_ones(f16x2 v, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(v, one, acc, false);
+}
+template <typename X8>
+__device__ __forceinline__ void sum8_into(const X8& v, float (&acc)[4]) {
+  acc[0] = dot2_ones(__builtin_shufflevector(v, v, 0, 1), acc[0]);
+  acc[1] = dot2_ones(__builtin_shufflevector(v, v, 2, 3), acc[1]);
+  acc[2] = dot2_ones(__builtin_shufflevector(v, v, 4, 5), acc[2]);
+  acc[3] = dot2_ones(__builtin_shufflevector(v, v, 6, 7), acc[3]);
+}
+
 // All-reduce across the two 32-lane halves of a wave.
 __device__ __forceinline__ float half_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -115,7 +134,8 @@ struct FwdParams {
   const int32_t* cu_k;
   int B, Hq, Hkv, Nq, Nk, D;
   int num_q_tiles;
-  float scale_log2;  // sm_scale * log2(e)
+  float scale_log2;  // |sm_scale| * log2(e), at least 1e-30
+  int neg_q;         // sm_scale < 0: q is negated on load so scale_log2 stays positive
 };
 
 struct BwdParams {

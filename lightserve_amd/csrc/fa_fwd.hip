@@ -6,13 +6,20 @@
 // computed and scaled, masked to -inf (key beyond the sequence, or causal),
 // the running row max is raised, p = exp(s - m) and alpha = exp(m_old - m),
 // l = alpha*l + sum(p), acc = alpha*acc + p(cast to the input dtype) @ V; at
-// the end o = acc / l and lse = m + ln(l).
+// the end o = acc / l and lse = m + ln(l). One difference in bookkeeping, not
+// in the result: the running max used as the exponent offset is only raised
+// when a row's tile max exceeds it by more than 2^8 (so p <= 256 and the
+// rescale of acc is skipped on most tiles); m + log(l) is unchanged by the
+// choice of offset.
 //
 // Work decomposition
 //   workgroup = 4 waves = 128 query rows of one (batch, head); wave w owns
-//   rows 32w..32w+31, one row per lane pair (l, l+32).
-//   K/V tiles of 64 keys are staged in LDS, double-buffered, 16-byte segments
-//   XOR-swizzled per row.
+//   rows 32w..32w+31, one row per lane pair (l, l+32). At most 256 registers
+//   per wave, so two workgroups share a CU and the hardware interleaves one
+//   wave's softmax with the other's MFMA work on each SIMD.
+//   K/V tiles of 64 keys go global -> LDS with buffer_load ... lds (no
+//   register staging; rows past the sequence read as zero through the buffer
+//   range check), double-buffered, 16-byte segments XOR-swizzled per row.
 //   S^T = K Q^T on MFMA (A = K rows from LDS, B = Q held in registers), so
 //   every lane owns one query row: the row max/sum need one permlane32 swap.
 //   The fp32 S^T accumulator is rounded in registers into the B operand of
@@ -22,23 +29,26 @@
 namespace lsfa {
 
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
-template <typename T, int DP, bool CAUSAL, bool VARLEN>
+template <typename T, int DP, bool CAUSAL, bool VARLEN, bool LSE>
 __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
-  constexpr int BM = 128, BN = 64, SEGS = DP / 8;
-  constexpr int TILE = BN * DP;
-  constexpr int CH = BN * SEGS / 256;  // 16-byte chunks per thread per tensor
+  constexpr int NW = 4, BM = NW * 32, BN = 64;
+  constexpr int TILE = BN * DP;              // elements of one K or V tile
+  constexpr int LDI = TILE * 2 / 1024 / NW;  // 1 KB direct loads per wave per tile
   constexpr int KSTEPS = DP / 16;
   constexpr int DT = DP / 32;
   constexpr int KB = BN / 32;
-  static_assert(CH >= 1, "tile too small for the workgroup");
+  static_assert(LDI >= 1, "tile too small for the workgroup");
 
-  __shared__ __attribute__((aligned(16))) T smem_raw[4 * TILE];
+  __shared__ __attribute__((aligned(1024))) T smem_raw[4 * TILE];  // K0 K1 V0 V1
   LDS_AS T* smem = (LDS_AS T*)smem_raw;
+  const LDS_AS char* sbytes = (const LDS_AS char*)smem_raw;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
   int bh, qt;
   map_tile(p.num_q_tiles, gridDim.x, bh, qt, CAUSAL);
@@ -61,6 +71,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   const T* V = (const T*)p.v + (VARLEN ? 0 : (int64_t)b * p.svb) + (int64_t)hk * p.svh + rk0 * p.svn;
   T* O = (T*)p.o + (VARLEN ? 0 : (int64_t)b * p.sob) + (int64_t)h * p.soh + rq0 * p.son;
 
+  // Buffer resources: every byte at or past row nk reads as zero.
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, (int)((int64_t)nk * p.skn * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, (int)((int64_t)nk * p.svn * 2), 0x00020000);
+
   int kv_end = nk;
   if (CAUSAL) kv_end = min(nk, q0 + BM + off);
   const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
@@ -68,131 +84,154 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   const int D = p.D;
   const int qw_lo = q0 + wave * 32;
   const int qrow = qw_lo + l32;
+  const float sl2 = p.scale_log2;  // > 0 (the host folds a negative scale into neg_q)
 
-  // Q as the B operand of S^T = K Q^T: lane holds row qrow, columns 16kk+8hh..+7.
+  // Q as the B operand of S^T = K Q^T: lane holds row qrow, columns
+  // 16kk + 8hh .. +7; zero outside the sequence / head dim.
   X8 qreg[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
     const int col = 16 * kk + 8 * hh;
     u32x4 raw = {0, 0, 0, 0};
     if (qrow < nq && col < D) raw = ldg16(Q + (int64_t)qrow * p.sqn + col);
+    if (p.neg_q) raw ^= 0x80008000u;
     qreg[kk] = __builtin_bit_cast(X8, raw);
   }
 
-  u32x4 kst[CH], vst[CH];
-  auto gload = [&](int j) {
+  // Direct global -> LDS tile load: wave w issues LDI 1 KB chunks; lane t of
+  // chunk c lands at tile byte (w*LDI + c)*1024 + 16t = (row, swizzled seg).
+  auto tile_load = [&](const __amdgpu_buffer_rsrc_t& rs, int64_t sn, int j, int buf) {
+    LDS_AS char* dst = (LDS_AS char*)(smem + buf * TILE);
 #pragma unroll
-    for (int r = 0; r < CH; ++r) {
-      const int c = tid + 256 * r;
-      const int row = c / SEGS, col = (c % SEGS) * 8;
-      const int key = j * BN + row;
-      const bool ok = key < nk && col < D;
-      kst[r] = ok ? ldg16(K + (int64_t)key * p.skn + col) : u32x4{0, 0, 0, 0};
-      vst[r] = ok ? ldg16(V + (int64_t)key * p.svn + col) : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < LDI; ++c) {
+      const int byte = (wave * LDI + c) * 1024 + lane * 16;
+      const int row = byte / (DP * 2);
+      const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+      const int voff = (int)(((int64_t)(j * BN + row) * sn + seg * 8) * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(dst + (wave * LDI + c) * 1024), 16, voff, 0, 0, 0);
     }
   };
-  auto sstore = [&](int stage) {
-    LDS_AS T* Ks = smem + stage * 2 * TILE;
-    LDS_AS T* Vs = Ks + TILE;
+
+  // Per-lane LDS byte offsets relative to a tile base. The swizzle depends
+  // only on row & 15, so the 32-row key block and 16-row steps are immediates.
+  int koff[KSTEPS];
 #pragma unroll
-    for (int r = 0; r < CH; ++r) {
-      const int c = tid + 256 * r;
-      const int row = c / SEGS, col = (c % SEGS) * 8;
-      const int o = swz_off<DP>(row, col);
-      *(LDS_AS u32x4*)(Ks + o) = kst[r];
-      *(LDS_AS u32x4*)(Vs + o) = vst[r];
-    }
-  };
+  for (int kk = 0; kk < KSTEPS; ++kk) koff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
+  const int tr_row = 4 * hh + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int voff[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    voff[dt][0] = swz_off<DP>(tr_row, 32 * dt + tr_col) * 2;
+    voff[dt][1] = swz_off<DP>(tr_row + 8, 32 * dt + tr_col) * 2;
+  }
 
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
-  float m = -INFINITY, l = 0.f;
-  const float sl2 = p.scale_log2;
+  // l_run: sum of the rounded p (normalises O); l_lse: sum of the fp32 p
+  // (kept only for the logsumexp output, as the reference's l_i).
+  float m_run = -1e30f, l_run = 0.f, l_lse = 0.f;
+
+  // Exponentials, rounding to the input dtype, row sum and O^T += V^T P^T.
+  // The row sum adds the rounded p that the MFMA multiplies (v_dot2 with
+  // ones), so numerator and denominator share the rounding of the dominant
+  // terms whatever the exponent offset.
+  auto body = [&](const LDS_AS char* Vs, f32x16 (&s)[KB]) {
+    const float neg_m = -m_run;
+    float rs[4] = {0.f, 0.f, 0.f, 0.f};
+    float re = 0.f;
+    X8 pb[2 * KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[kb][i] = fast_exp2(fmaf(s[kb][i], sl2, neg_m));
+        if constexpr (LSE) re += s[kb][i];
+      }
+      pb[2 * kb] = pack8<T>(s[kb], 0);
+      pb[2 * kb + 1] = pack8<T>(s[kb], 8);
+      sum8_into(pb[2 * kb], rs);
+      sum8_into(pb[2 * kb + 1], rs);
+    }
+    l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+    if constexpr (LSE) l_lse += re;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int ks = 0; ks < 2 * KB; ++ks) {
+        const LDS_AS char* base = Vs + ks * 16 * DP * 2;
+        const X8 a = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(base + voff[dt][0])),
+                                  lds_read_tr((const LDS_AS T*)(base + voff[dt][1])));
+        acc[dt] = mfma32(a, pb[ks], acc[dt]);
+      }
+    }
+  };
 
   if (ntiles > 0) {
-    gload(0);
-    sstore(0);
+    tile_load(krs, p.skn, 0, 0);
+    tile_load(vrs, p.svn, 0, 2);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  // Per-lane constant parts of the LDS addresses.
-  const int tr_row = 4 * hh + ((lane & 15) >> 2);
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-
   for (int j = 0; j < ntiles; ++j) {
-    if (j + 1 < ntiles) gload(j + 1);
+    if (j + 1 < ntiles) {
+      tile_load(krs, p.skn, j + 1, (j + 1) & 1);
+      tile_load(vrs, p.svn, j + 1, 2 + ((j + 1) & 1));
+    }
     const int kbase = j * BN;
     const bool active = !CAUSAL || (kbase <= qw_lo + 31 + off);
     if (active) {
-      const LDS_AS T* Ks = smem + (j & 1) * 2 * TILE;
-      const LDS_AS T* Vs = Ks + TILE;
+      const LDS_AS char* Ks = sbytes + (j & 1) * TILE * 2;
+      const LDS_AS char* Vs = sbytes + (2 + (j & 1)) * TILE * 2;
       f32x16 s[KB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        s[kb] = f32x16{};
+      for (int kb = 0; kb < KB; ++kb) s[kb] = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          X8 a = lds_read8<T>(Ks + swz_off<DP>(kb * 32 + l32, 16 * kk + 8 * hh));
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const X8 a = *(const LDS_AS X8*)(Ks + kb * 32 * DP * 2 + koff[kk]);
           s[kb] = mfma32(a, qreg[kk], s[kb]);
         }
       }
       const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > qw_lo + off);
-      float mx = -INFINITY;
+      if (need_mask) {
+        int lim = nk - 1 - kbase - 4 * hh;
+        if (CAUSAL) lim = min(lim, qrow + off - kbase - 4 * hh);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float t = s[kb][i] * sl2;
-          if (need_mask) {
-            const int key = kbase + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-            if (key >= nk || (CAUSAL && key > qrow + off)) t = -INFINITY;
-          }
-          s[kb][i] = t;
-          mx = fmaxf(mx, t);
-        }
+          for (int i = 0; i < 16; ++i)
+            if (32 * kb + 8 * (i >> 2) + (i & 3) > lim) s[kb][i] = -INFINITY;
       }
+      float mx = s[0][0];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
       mx = half_max(mx);
-      const float m_new = fmaxf(m, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m - m_use);
-      float rs = 0.f;
+      const float mxs = mx == -INFINITY ? -INFINITY : mx * sl2;
+      // Raise the running offset only where a row max moved by more than the
+      // threshold (wave-uniform branch, taken on few tiles): O and l rescale
+      // in place.
+      if (__builtin_amdgcn_ballot_w64(mxs > m_run + kRescaleThreshold) != 0) {
+        const float m_new = fmaxf(m_run, mxs);
+        const float alpha = fast_exp2(m_run - m_new);
+        l_run *= alpha;
+        if constexpr (LSE) l_lse *= alpha;
+        m_run = m_new;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = fast_exp2(s[kb][i] - m_use);
-          s[kb][i] = e;
-          rs += e;
-        }
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
       }
-      l = l * alpha + rs;
-      m = m_new;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-      X8 pb[2 * KB];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        pb[2 * kb] = pack8<T>(s[kb], 0);
-        pb[2 * kb + 1] = pack8<T>(s[kb], 8);
-      }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-        for (int ks = 0; ks < 2 * KB; ++ks) {
-          const int row = ks * 16 + tr_row;
-          const int col = 32 * dt + tr_col;
-          X4 a0 = lds_read_tr(Vs + swz_off<DP>(row, col));
-          X4 a1 = lds_read_tr(Vs + swz_off<DP>(row + 8, col));
-          acc[dt] = mfma32(cat4<X8, X4>(a0, a1), pb[ks], acc[dt]);
-        }
-      }
+      body(Vs, s);
     }
-    if (j + 1 < ntiles) sstore((j + 1) & 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 
-  const float lt = half_sum(l);
+  const float lt = half_sum(l_run);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   if (qrow < nq) {
     T* orow = O + (int64_t)qrow * p.son;
@@ -209,9 +248,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
         }
       }
     }
-    if (p.lse != nullptr && hh == 0) {
-      float* L = p.lse + (VARLEN ? 0 : (int64_t)b * p.slb) + (int64_t)h * p.slh + (rq0 + qrow) * p.sln;
-      *L = lt > 0.f ? (m + __log2f(lt)) * kLn2 : -INFINITY;
+    if constexpr (LSE) {
+      const float le = half_sum(l_lse);
+      if (hh == 0) {
+        float* L = p.lse + (VARLEN ? 0 : (int64_t)b * p.slb) + (int64_t)h * p.slh + (rq0 + qrow) * p.sln;
+        *L = le > 0.f ? (m_run + __log2f(le)) * kLn2 : -INFINITY;
+      }
     }
   }
 }
@@ -219,7 +261,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
 template <typename T, int DP, bool CAUSAL, bool VARLEN>
 static hipError_t launch_fwd(const FwdParams& p, hipStream_t s) {
   const int total = p.num_q_tiles * p.B * p.Hq;
-  hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN>), dim3(total), dim3(256), 0, s, p);
+  if (p.lse != nullptr)
+    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, true>), dim3(total), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, false>), dim3(total), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
@@ -239,7 +284,7 @@ static hipError_t dispatch_fwd_t(const FwdParams& p, int dp, bool causal, bool v
 }
 
 // Host entry used by the C ABI layer. is_bf16 selects bf16 vs fp16 operands;
-// dp is the padded head dim (32, 64 or 128). Query tile height is 128 rows.
+// dp is the padded head dim (32, 64 or 128). Query tiles are 128 rows.
 hipError_t fwd_mfma(FwdParams p, bool is_bf16, int dp, bool causal, bool varlen, hipStream_t s) {
   p.num_q_tiles = (p.Nq + 127) / 128;
   if (is_bf16) return dispatch_fwd_t<__bf16>(p, dp, causal, varlen, s);
