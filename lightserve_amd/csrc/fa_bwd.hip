@@ -203,33 +203,54 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV. Workgroup = 4 waves x 32 keys; query tiles of 64 rows (Q, dO, and
-// the per-row L and delta) double-buffered in LDS. Per query tile and wave,
-// for each 32-row half qb:
-//   S  = Q K^T            A = Q rows (LDS),  B = K^T (registers)
-//   dP = dO V^T           A = dO rows (LDS), B = V^T (registers)
+// dK, dV. Workgroup = 8 waves (two per SIMD, at most 256 registers each)
+// over 128 keys. K and V of those keys stay in LDS for the whole kernel.
+// Query tiles of 64 rows are staged in LDS twice: row-major (A operand of
+// S = Q K^T and dP = dO V^T) and transposed with the row order permuted so
+// that each MFMA operand of dV^T += dO^T P and dK^T += Q^T dS is a single
+// ds_read_b128 (no transpose reads in the loop). Wave w owns keys
+// 32*(w%4)..+31 and query rows 32*(w/4)..+31 of every tile:
+//   S  = Q K^T            A = Q rows (LDS),   B = K rows (LDS)
+//   dP = dO V^T           A = dO rows (LDS),  B = V rows (LDS)
 //   P  = exp2(S*scale*log2e - L*log2e), dS = P (dP - delta)
-//   dV^T += dO^T P        A = dO^T via transpose reads, B = P (registers)
-//   dK^T += Q^T dS        A = Q^T via transpose reads,  B = dS (registers)
+//   dV^T += dO^T P        A = dO^T (LDS),     B = P  (registers)
+//   dK^T += Q^T dS        A = Q^T (LDS),      B = dS (registers)
+// The two query halves' partial dK/dV are summed through LDS at the end.
 // Query rows beyond the sequence get L = +inf, so their P is exactly 0.
 // ---------------------------------------------------------------------------
+
+// Position of tile-local query q (0..63) in a transposed tile row: bits 2
+// and 3 swap, so that the 8 queries one lane half feeds to a 32x32x16 MFMA
+// (16*kk + 8*(s/4) + 4*h + s%4, s = 0..7) sit in 16 contiguous bytes.
+__device__ __forceinline__ int tpos(int q) { return (q & ~12) | ((q & 4) << 1) | ((q & 8) >> 1); }
+// Byte offset of (row d, position pos) in a transposed [DP][64] tile; the
+// 16-byte column is XOR-swizzled with (d/2)%8 so 16 consecutive rows read
+// at one column hit distinct banks.
+__device__ __forceinline__ int toff(int d, int pos) { return d * 128 + ((((pos >> 3) ^ ((d >> 1) & 7))) << 4) + (pos & 7) * 2; }
+
 template <typename T, int DP, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
+__global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
-  using X4 = typename VecT<T>::x4;
-  constexpr int BNK = 128, BMQ = 64, SEGS = DP / 8;
-  constexpr int TILE = BMQ * DP;
-  constexpr int CH = BMQ * SEGS / 256;
+  constexpr int NW = 8, BNK = 128, BMQ = 64;
+  constexpr int SEGS = DP / 8;
   constexpr int KSTEPS = DP / 16;
   constexpr int DT = DP / 32;
-  constexpr int STAGE = 2 * TILE * (int)sizeof(T) + 2 * BMQ * 4;  // bytes
-
-  __shared__ __attribute__((aligned(16))) char smem_raw[2 * STAGE];
-  LDS_AS char* smem = (LDS_AS char*)smem_raw;
+  constexpr int KV_BYTES = BNK * DP * 2;               // one of K or V
+  constexpr int QT_BYTES = BMQ * DP * 2;               // one Q-side tile (any layout)
+  constexpr int UNITS = (BMQ / 4) * SEGS;              // 4-row x 8-column units per tensor
+  constexpr int LDI = KV_BYTES / 1024 / NW;            // direct 1 KB loads per wave for K or V
+  static_assert(LDI >= 1 && UNITS <= 256, "tile shape");
+  // LDS: K | V | Qr | dOr | Qt | dOt | L | delta
+  constexpr int OFF_K = 0, OFF_V = KV_BYTES, OFF_QR = 2 * KV_BYTES, OFF_OR = OFF_QR + QT_BYTES;
+  constexpr int OFF_QT = OFF_OR + QT_BYTES, OFF_OT = OFF_QT + QT_BYTES, OFF_L = OFF_OT + QT_BYTES;
+  constexpr int LDS_BYTES = OFF_L + 2 * BMQ * 4;
+  __shared__ __attribute__((aligned(1024))) char smem_raw[LDS_BYTES];
+  LDS_AS char* sm = (LDS_AS char*)smem_raw;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
+  const int kbw = wave & 3, qh = wave >> 2;  // key block and query half of this wave
   int bh, kt;
   map_tile(p.num_tiles, gridDim.x, bh, kt, false);
   const int b = bh / p.H, h = bh - b * p.H;
@@ -238,29 +259,31 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   const int off = nk - nq;
 
   const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
-  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh;
-  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh;
+  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh + (int64_t)k0 * p.skn;
+  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh + (int64_t)k0 * p.svn;
   const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
   T* dK = (T*)p.dk + (int64_t)b * p.sdkb + (int64_t)h * p.sdkh;
   T* dV = (T*)p.dv + (int64_t)b * p.sdvb + (int64_t)h * p.sdvh;
   const float* Lg = p.lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
   const float* Dg = p.delta + (int64_t)b * p.slb + (int64_t)h * p.slh;
 
-  const int kw_lo = k0 + wave * 32;
-  const int krow = kw_lo + l32;
-  const bool kvalid = krow < nk;
-
-  X8 kreg[KSTEPS], vreg[KSTEPS];
+  // K and V of the 128 keys: direct loads, zero past the sequence end.
+  {
+    const int kn = max(0, min(BNK, nk - k0));
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, (int)((int64_t)kn * p.skn * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, (int)((int64_t)kn * p.svn * 2), 0x00020000);
 #pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) {
-    const int col = 16 * kk + 8 * hh;
-    u32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
-    if (kvalid && col < D) {
-      rk = ldg16(K + (int64_t)krow * p.skn + col);
-      rv = ldg16(V + (int64_t)krow * p.svn + col);
+    for (int c = 0; c < LDI; ++c) {
+      const int byte = (wave * LDI + c) * 1024 + lane * 16;
+      const int row = byte / (DP * 2);
+      const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (LDS_AS void*)(sm + OFF_K + (wave * LDI + c) * 1024), 16,
+                                               (int)(((int64_t)row * p.skn + seg * 8) * 2), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (LDS_AS void*)(sm + OFF_V + (wave * LDI + c) * 1024), 16,
+                                               (int)(((int64_t)row * p.svn + seg * 8) * 2), 0, 0, 0);
     }
-    kreg[kk] = __builtin_bit_cast(X8, rk);
-    vreg[kk] = __builtin_bit_cast(X8, rv);
   }
 
   // Query range that can see this key tile.
@@ -269,44 +292,62 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   q_lo = (q_lo / BMQ) * BMQ;
   const int ntiles = (nq > q_lo) ? (nq - q_lo + BMQ - 1) / BMQ : 0;
 
-  u32x4 qst[CH], dost[CH];
-  float lst = 0.f;
+  // Staging: thread t < 2*UNITS loads one 4-row x 8-column unit of Q (t <
+  // UNITS) or dO; threads 0..15 also load 4 values of L, threads 16..31 of
+  // delta.
+  const bool is_do = tid >= UNITS;
+  const int u = is_do ? tid - UNITS : tid;
+  const bool stager = tid < 2 * UNITS;
+  const int g4 = u % (BMQ / 4), dseg = u / (BMQ / 4);
+  const T* src = is_do ? dO : Q;
+  const int64_t sstride = is_do ? p.sdon : p.sqn;
+  u32x4 st[4];
+  f32x4 lst = {0.f, 0.f, 0.f, 0.f};
+  const int lrow = tid;  // 0..15: L, 16..31: delta
   auto gload = [&](int t) {
     const int qs = q_lo + t * BMQ;
+    if (stager) {
 #pragma unroll
-    for (int r = 0; r < CH; ++r) {
-      const int c = tid + 256 * r;
-      const int row = c / SEGS, col = (c % SEGS) * 8;
-      const int q = qs + row;
-      const bool ok = q < nq && col < D;
-      qst[r] = ok ? ldg16(Q + (int64_t)q * p.sqn + col) : u32x4{0, 0, 0, 0};
-      dost[r] = ok ? ldg16(dO + (int64_t)q * p.sdon + col) : u32x4{0, 0, 0, 0};
+      for (int r = 0; r < 4; ++r) {
+        const int q = qs + 4 * g4 + r;
+        st[r] = (q < nq && dseg * 8 < D) ? ldg16(src + (int64_t)q * sstride + dseg * 8) : u32x4{0, 0, 0, 0};
+      }
     }
-    if (tid < 2 * BMQ) {
-      const int q = qs + (tid & (BMQ - 1));
-      if (tid < BMQ) {
-        float lv = q < nq ? Lg[(int64_t)q * p.sln] : INFINITY;
-        if (lv == -INFINITY) lv = INFINITY;
-        lst = lv * kLog2eB;
-      } else {
-        lst = q < nq ? Dg[(int64_t)q * p.sln] : 0.f;
+    if (lrow < 32) {
+      const int base = qs + 4 * (lrow & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int q = base + e;
+        if (lrow < 16) {
+          float lv = q < nq ? Lg[(int64_t)q * p.sln] : INFINITY;
+          if (lv == -INFINITY) lv = INFINITY;  // row saw no key: P == 0
+          lst[e] = lv * 1.4426950408889634f;
+        } else {
+          lst[e] = q < nq ? Dg[(int64_t)q * p.sln] : 0.f;
+        }
       }
     }
   };
-  auto sstore = [&](int stage) {
-    LDS_AS char* base = smem + stage * STAGE;
-    LDS_AS T* Qs = (LDS_AS T*)base;
-    LDS_AS T* dOs = Qs + TILE;
-    LDS_AS float* Ls = (LDS_AS float*)(dOs + TILE);
+  auto sstore = [&]() {
+    if (stager) {
+      const int qr = is_do ? OFF_OR : OFF_QR;
+      const int qt = is_do ? OFF_OT : OFF_QT;
 #pragma unroll
-    for (int r = 0; r < CH; ++r) {
-      const int c = tid + 256 * r;
-      const int row = c / SEGS, col = (c % SEGS) * 8;
-      const int o = swz_off<DP>(row, col);
-      *(LDS_AS u32x4*)(Qs + o) = qst[r];
-      *(LDS_AS u32x4*)(dOs + o) = dost[r];
+      for (int r = 0; r < 4; ++r)
+        *(LDS_AS u32x4*)(sm + qr + swz_off<DP>(4 * g4 + r, dseg * 8) * 2) = st[r];
+      // Transposed: row d = 8*dseg + i holds the 4 queries' values of column i.
+      const int pos = tpos(4 * g4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int w = i >> 1, sh = (i & 1) * 16;
+        const uint32_t lo = ((st[0][w] >> sh) & 0xffffu) | (((st[1][w] >> sh) & 0xffffu) << 16);
+        const uint32_t hi = ((st[2][w] >> sh) & 0xffffu) | (((st[3][w] >> sh) & 0xffffu) << 16);
+        *(LDS_AS u32x2*)(sm + qt + toff(dseg * 8 + i, pos)) = u32x2{lo, hi};
+      }
     }
-    if (tid < 2 * BMQ) Ls[tid] = lst;
+    if (lrow < 32) {
+      *(LDS_AS f32x4*)(sm + OFF_L + lrow * 16) = lst;
+    }
   };
 
   f32x16 dk[DT], dv[DT];
@@ -316,88 +357,112 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     dv[dt] = f32x16{};
   }
   const float sl2 = p.scale_log2;
-  const int tr_row = 4 * hh + ((lane & 15) >> 2);
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int krow = k0 + 32 * kbw + l32;  // key owned by this lane (C-layout column)
+  int aoff[KSTEPS];                      // Q/dO rows (A) and K/V rows (B): same swizzle
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) aoff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
+  int toffs[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int kk2 = 0; kk2 < 2; ++kk2) toffs[dt][kk2] = toff(32 * dt + l32, 32 * qh + 16 * kk2 + 8 * hh);
 
-  if (ntiles > 0) {
-    gload(0);
-    sstore(0);
-  }
-  __syncthreads();
-
+  if (ntiles > 0) gload(0);
   for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();  // previous tile fully consumed (and K/V resident on t = 0)
+    sstore();
+    if (t == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     if (t + 1 < ntiles) gload(t + 1);
     const int qs = q_lo + t * BMQ;
-    // Causal: every key of this wave is beyond every query of the tile.
-    const bool active = !CAUSAL || (qs + BMQ - 1 + off >= kw_lo);
-    if (active) {
-      LDS_AS char* base = smem + (t & 1) * STAGE;
-      const LDS_AS T* Qs = (const LDS_AS T*)base;
-      const LDS_AS T* dOs = Qs + TILE;
-      const LDS_AS float* Ls = (const LDS_AS float*)(dOs + TILE);
-      const LDS_AS float* Ds = Ls + BMQ;
-      const bool need_mask = CAUSAL && (qs + off < kw_lo + 31);
+    const int qw = qs + 32 * qh;          // first query row of this wave
+    const int kw = k0 + 32 * kbw;         // first key of this wave
+    // Tiles where every key of the wave lies after every query row are not
+    // skipped: the causal mask zeroes their P and dS (they only occur among
+    // the first tiles of the sweep), which keeps the loop body branch-free
+    // apart from the mask itself.
+    f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
-      for (int qb = 0; qb < BMQ / 32; ++qb) {
-        f32x16 s = f32x16{}, dp = f32x16{};
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const X8 aq = *(const LDS_AS X8*)(sm + OFF_QR + 32 * qh * DP * 2 + aoff[kk]);
+      const X8 ao = *(const LDS_AS X8*)(sm + OFF_OR + 32 * qh * DP * 2 + aoff[kk]);
+      const X8 bk = *(const LDS_AS X8*)(sm + OFF_K + 32 * kbw * DP * 2 + aoff[kk]);
+      const X8 bv = *(const LDS_AS X8*)(sm + OFF_V + 32 * kbw * DP * 2 + aoff[kk]);
+      s = mfma32(aq, bk, s);
+      dp = mfma32(ao, bv, dp);
+    }
+    // Register 4g+e holds query qw + 8g + 4hh + e of this lane's key.
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          const int o = swz_off<DP>(qb * 32 + l32, 16 * kk + 8 * hh);
-          s = mfma32(lds_read8<T>(Qs + o), kreg[kk], s);
-          dp = mfma32(lds_read8<T>(dOs + o), vreg[kk], dp);
-        }
+    for (int g = 0; g < 4; ++g) {
+      const int qi = 32 * qh + 8 * g + 4 * hh;
+      const f32x4 lv = *(const LDS_AS f32x4*)(sm + OFF_L + qi * 4);
+      const f32x4 dl = *(const LDS_AS f32x4*)(sm + OFF_L + BMQ * 4 + qi * 4);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int qi = qb * 32 + 8 * g + 4 * hh;  // tile-local row of register 4g
-          const f32x4 lv = *(const LDS_AS f32x4*)(Ls + qi);
-          const f32x4 dl = *(const LDS_AS f32x4*)(Ds + qi);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float pv = fast_exp2(s[4 * g + e] * sl2 - lv[e]);
-            if (need_mask && krow > qs + qi + e + off) pv = 0.f;
-            s[4 * g + e] = pv;
-            dp[4 * g + e] = pv * (dp[4 * g + e] - dl[e]);
-          }
-        }
-        const X8 pb0 = pack8<T>(s, 0), pb1 = pack8<T>(s, 8);
-        const X8 db0 = pack8<T>(dp, 0), db1 = pack8<T>(dp, 8);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int col = 32 * dt + tr_col;
-#pragma unroll
-          for (int kk2 = 0; kk2 < 2; ++kk2) {
-            const int row = qb * 32 + kk2 * 16 + tr_row;
-            const int o0 = swz_off<DP>(row, col), o1 = swz_off<DP>(row + 8, col);
-            const X8 doT = cat4<X8, X4>(lds_read_tr(dOs + o0), lds_read_tr(dOs + o1));
-            const X8 qT = cat4<X8, X4>(lds_read_tr(Qs + o0), lds_read_tr(Qs + o1));
-            dv[dt] = mfma32(doT, kk2 ? pb1 : pb0, dv[dt]);
-            dk[dt] = mfma32(qT, kk2 ? db1 : db0, dk[dt]);
-          }
-        }
+      for (int e = 0; e < 4; ++e) {
+        const float pv = fast_exp2(fmaf(s[4 * g + e], sl2, -lv[e]));
+        s[4 * g + e] = pv;
+        dp[4 * g + e] = pv * (dp[4 * g + e] - dl[e]);
       }
     }
-    if (t + 1 < ntiles) sstore((t + 1) & 1);
-    __syncthreads();
+    if (CAUSAL && qw + off < kw + 31) {  // tile crosses the diagonal: drop keys after the query
+      const int lim = krow - off - qw - 4 * hh;  // masked if 8(i/4) + i%4 < lim
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const bool m = 8 * (i >> 2) + (i & 3) < lim;
+        s[i] = m ? 0.f : s[i];
+        dp[i] = m ? 0.f : dp[i];
+      }
+    }
+    const X8 pb0 = pack8<T>(s, 0), pb1 = pack8<T>(s, 8);
+    const X8 db0 = pack8<T>(dp, 0), db1 = pack8<T>(dp, 8);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const X8 ao0 = *(const LDS_AS X8*)(sm + OFF_OT + toffs[dt][0]);
+      const X8 ao1 = *(const LDS_AS X8*)(sm + OFF_OT + toffs[dt][1]);
+      const X8 aq0 = *(const LDS_AS X8*)(sm + OFF_QT + toffs[dt][0]);
+      const X8 aq1 = *(const LDS_AS X8*)(sm + OFF_QT + toffs[dt][1]);
+      dv[dt] = mfma32(ao0, pb0, dv[dt]);
+      dk[dt] = mfma32(aq0, db0, dk[dt]);
+      dv[dt] = mfma32(ao1, pb1, dv[dt]);
+      dk[dt] = mfma32(aq1, db1, dk[dt]);
+    }
   }
 
-  if (kvalid) {
-    T* krow_k = dK + (int64_t)krow * p.sdkn;
-    T* krow_v = dV + (int64_t)krow * p.sdvn;
+  // Sum the two query halves: waves 4..7 park their partials in LDS (over
+  // K/V, whose direct loads must have landed even if no tile ran).
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  LDS_AS f32x4* park = (LDS_AS f32x4*)sm;  // (4 waves) x (2*DT*4) x 64 lanes x 16 B <= 128 KB
+  if (qh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        park[((kbw * 2 * DT + dt) * 4 + g) * 64 + lane] = f32x4{dk[dt][4 * g], dk[dt][4 * g + 1], dk[dt][4 * g + 2], dk[dt][4 * g + 3]};
+        park[(((kbw * 2 + 1) * DT + dt) * 4 + g) * 64 + lane] = f32x4{dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3]};
+      }
+  }
+  __syncthreads();
+  if (qh == 0 && krow < nk) {
+    T* rk = dK + (int64_t)krow * p.sdkn;
+    T* rv = dV + (int64_t)krow * p.sdvn;
     const float sc = p.scale;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        const f32x4 ok = park[((kbw * 2 * DT + dt) * 4 + g) * 64 + lane];
+        const f32x4 ov = park[(((kbw * 2 + 1) * DT + dt) * 4 + g) * 64 + lane];
         const int d = 32 * dt + 8 * g + 4 * hh;
         if (d < D) {
-          X4 a, c;
+          typename VecT<T>::x4 a, c;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            a[e] = (T)(dk[dt][4 * g + e] * sc);
-            c[e] = (T)dv[dt][4 * g + e];
+            a[e] = (T)((dk[dt][4 * g + e] + ok[e]) * sc);
+            c[e] = (T)(dv[dt][4 * g + e] + ov[e]);
           }
-          *(X4*)(krow_k + d) = a;
-          *(X4*)(krow_v + d) = c;
+          *(typename VecT<T>::x4*)(rk + d) = a;
+          *(typename VecT<T>::x4*)(rv + d) = c;
         }
       }
     }
@@ -415,7 +480,7 @@ static hipError_t launch_bwd(BwdParams p, hipStream_t s) {
   }
   p.num_tiles = (p.Nk + 127) / 128;
   if (p.num_tiles > 0) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(512), 0, s, p);
     return hipGetLastError();
   }
   return hipSuccess;
