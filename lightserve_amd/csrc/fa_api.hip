@@ -48,6 +48,10 @@ int check_fast_layout(const char* name, const void* ptr, const int64_t* st, bool
     if (st[i] % 8 != 0)
       return fail(LSFA_ERR_UNSUPPORTED, "%s: stride[%d]=%lld is not a multiple of 8 elements", name, i, (long long)st[i]);
   if (!aligned16(ptr)) return fail(LSFA_ERR_UNSUPPORTED, "%s: base pointer is not 16-byte aligned", name);
+  // Tile loads address up to 128 rows from a per-tile base with 32-bit byte
+  // offsets.
+  if (st[2] < 0 || st[2] > (1LL << 22))
+    return fail(LSFA_ERR_UNSUPPORTED, "%s: row stride %lld outside 0..2^22 elements", name, (long long)st[2]);
   return LSFA_OK;
 }
 

@@ -23,26 +23,29 @@ namespace lsfa {
 constexpr float kLog2eB = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
-// dQ (and delta). Workgroup = 4 waves x 32 query rows; K/V tiles of 64 keys
-// double-buffered in LDS. Per key tile and wave:
+// dQ (and delta). Workgroup = 4 waves x 32 query rows, at most 256 registers
+// per wave so two workgroups share a CU. K/V tiles of 64 keys go global ->
+// LDS with buffer_load ... lds (double-buffered, zero past the sequence end).
+// Per key tile and wave:
 //   S^T  = K Q^T          A = K rows (LDS),  B = Q^T  (registers)
 //   dP^T = V dO^T         A = V rows (LDS),  B = dO^T (registers)
 //   dS^T = P^T (dP^T - delta)  -> rounded into B operands
 //   dQ^T += K^T dS^T      A = K^T via transpose reads of the same LDS tile
 // ---------------------------------------------------------------------------
 template <typename T, int DP, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
-  constexpr int BM = 128, BN = 64, SEGS = DP / 8;
+  constexpr int NW = 4, BM = NW * 32, BN = 64;
   constexpr int TILE = BN * DP;
-  constexpr int CH = BN * SEGS / 256;
+  constexpr int LDI = TILE * 2 / 1024 / NW;
   constexpr int KSTEPS = DP / 16;
   constexpr int DT = DP / 32;
   constexpr int KB = BN / 32;
+  static_assert(LDI >= 1, "tile too small for the workgroup");
 
-  __shared__ __attribute__((aligned(16))) T smem_raw[4 * TILE];
-  LDS_AS T* smem = (LDS_AS T*)smem_raw;
+  __shared__ __attribute__((aligned(1024))) T smem_raw[4 * TILE];  // K0 K1 V0 V1
+  LDS_AS char* sm = (LDS_AS char*)smem_raw;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -94,92 +97,104 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const BwdParams p) {
   if (CAUSAL) kv_end = min(nk, q0 + BM + off);
   const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
-  u32x4 kst[CH], vst[CH];
-  auto gload = [&](int j) {
+  // Direct tile loads: lane t of chunk c fills LDS bytes [16t, 16t+16) of
+  // that chunk, i.e. stored segment (byte % 2DP)/16 of a tile row, which holds
+  // logical segment stored ^ seg_swz(row). The buffer descriptor is rebuilt
+  // per tile (scalar work) and clipped to the rows that exist, so the
+  // per-lane byte offsets are loop-invariant and rows past nk read as zero.
+  int kvo[LDI], vvo[LDI];
 #pragma unroll
-    for (int r = 0; r < CH; ++r) {
-      const int c = tid + 256 * r;
-      const int row = c / SEGS, col = (c % SEGS) * 8;
-      const int key = j * BN + row;
-      const bool ok = key < nk && col < D;
-      kst[r] = ok ? ldg16(K + (int64_t)key * p.skn + col) : u32x4{0, 0, 0, 0};
-      vst[r] = ok ? ldg16(V + (int64_t)key * p.svn + col) : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto sstore = [&](int stage) {
-    LDS_AS T* Ks = smem + stage * 2 * TILE;
-    LDS_AS T* Vs = Ks + TILE;
+  for (int c = 0; c < LDI; ++c) {
+    const int byte = (wave * LDI + c) * 1024 + lane * 16;
+    const int row = byte / (DP * 2);
+    const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+    kvo[c] = (int)(row * p.skn * 2) + seg * 16;
+    vvo[c] = (int)(row * p.svn * 2) + seg * 16;
+  }
+  auto tile_load = [&](const T* base, int64_t sn, const int* vo, int j, int buf) {
+    const int rows = min(nk - j * BN, BN);
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base + (int64_t)j * BN * sn, (int)(rows * sn * 2));
+    LDS_AS char* dst = sm + buf * TILE * 2;
 #pragma unroll
-    for (int r = 0; r < CH; ++r) {
-      const int c = tid + 256 * r;
-      const int row = c / SEGS, col = (c % SEGS) * 8;
-      const int o = swz_off<DP>(row, col);
-      *(LDS_AS u32x4*)(Ks + o) = kst[r];
-      *(LDS_AS u32x4*)(Vs + o) = vst[r];
-    }
+    for (int c = 0; c < LDI; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(dst + (wave * LDI + c) * 1024), 16, vo[c], 0, 0, 0);
   };
+
+  int koff[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) koff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
+  const int tr_row = 4 * hh + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int troff[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    troff[dt][0] = swz_off<DP>(tr_row, 32 * dt + tr_col) * 2;
+    troff[dt][1] = swz_off<DP>(tr_row + 8, 32 * dt + tr_col) * 2;
+  }
 
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
   const float sl2 = p.scale_log2;
-  const int tr_row = 4 * hh + ((lane & 15) >> 2);
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   if (ntiles > 0) {
-    gload(0);
-    sstore(0);
+    tile_load(K, p.skn, kvo, 0, 0);
+    tile_load(V, p.svn, vvo, 0, 2);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
   for (int j = 0; j < ntiles; ++j) {
-    if (j + 1 < ntiles) gload(j + 1);
+    if (j + 1 < ntiles) {
+      tile_load(K, p.skn, kvo, j + 1, (j + 1) & 1);
+      tile_load(V, p.svn, vvo, j + 1, 2 + ((j + 1) & 1));
+    }
     const int kbase = j * BN;
     const bool active = !CAUSAL || (kbase <= qw_lo + 31 + off);
     if (active) {
-      const LDS_AS T* Ks = smem + (j & 1) * 2 * TILE;
-      const LDS_AS T* Vs = Ks + TILE;
+      const LDS_AS char* Ks = sm + (j & 1) * TILE * 2;
+      const LDS_AS char* Vs = sm + (2 + (j & 1)) * TILE * 2;
       f32x16 s[KB], dp[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         s[kb] = f32x16{};
         dp[kb] = f32x16{};
+      }
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          const int o = swz_off<DP>(kb * 32 + l32, 16 * kk + 8 * hh);
-          s[kb] = mfma32(lds_read8<T>(Ks + o), qreg[kk], s[kb]);
-          dp[kb] = mfma32(lds_read8<T>(Vs + o), doreg[kk], dp[kb]);
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const int o = kb * 32 * DP * 2 + koff[kk];
+          s[kb] = mfma32(*(const LDS_AS X8*)(Ks + o), qreg[kk], s[kb]);
+          dp[kb] = mfma32(*(const LDS_AS X8*)(Vs + o), doreg[kk], dp[kb]);
         }
       }
-      const bool need_mask = CAUSAL && (kbase + BN - 1 > qw_lo + off);
-      X8 dsb[2 * KB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          float pv = fast_exp2(s[kb][i] * sl2 - l2);
-          if (need_mask) {
-            const int key = kbase + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-            if (key > qrow + off) pv = 0.f;
-          }
+          const float pv = fast_exp2(fmaf(s[kb][i], sl2, -l2));
           s[kb][i] = pv * (dp[kb][i] - delta);
         }
-        dsb[2 * kb] = pack8<T>(s[kb], 0);
-        dsb[2 * kb + 1] = pack8<T>(s[kb], 8);
+      if (CAUSAL && kbase + BN - 1 > qw_lo + off) {  // tile crosses the diagonal
+        const int lim = qrow + off - kbase - 4 * hh;  // masked if 32kb + 8(i/4) + i%4 > lim
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[kb][i] = (32 * kb + 8 * (i >> 2) + (i & 3) > lim) ? 0.f : s[kb][i];
       }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
         for (int ks = 0; ks < 2 * KB; ++ks) {
-          const int row = ks * 16 + tr_row;
-          const int col = 32 * dt + tr_col;
-          X4 a0 = lds_read_tr(Ks + swz_off<DP>(row, col));
-          X4 a1 = lds_read_tr(Ks + swz_off<DP>(row + 8, col));
-          acc[dt] = mfma32(cat4<X8, X4>(a0, a1), dsb[ks], acc[dt]);
+          const LDS_AS char* base = Ks + ks * 16 * DP * 2;
+          const X8 a = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(base + troff[dt][0])),
+                                    lds_read_tr((const LDS_AS T*)(base + troff[dt][1])));
+          acc[dt] = mfma32(a, pack8<T>(s[ks >> 1], 8 * (ks & 1)), acc[dt]);
         }
       }
     }
-    if (j + 1 < ntiles) sstore((j + 1) & 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 

@@ -181,4 +181,10 @@ __device__ __forceinline__ void map_tile(int num_tiles, int total, int& bh, int&
 
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *(const u32x4*)p; }
 
+// Raw buffer descriptor over [base, base + bytes): loads at or past the end
+// return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, 0x00020000);
+}
+
 }  // namespace lsfa

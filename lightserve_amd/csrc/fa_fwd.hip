@@ -71,12 +71,6 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   const T* V = (const T*)p.v + (VARLEN ? 0 : (int64_t)b * p.svb) + (int64_t)hk * p.svh + rk0 * p.svn;
   T* O = (T*)p.o + (VARLEN ? 0 : (int64_t)b * p.sob) + (int64_t)h * p.soh + rq0 * p.son;
 
-  // Buffer resources: every byte at or past row nk reads as zero.
-  const __amdgpu_buffer_rsrc_t krs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, (int)((int64_t)nk * p.skn * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, (int)((int64_t)nk * p.svn * 2), 0x00020000);
-
   int kv_end = nk;
   if (CAUSAL) kv_end = min(nk, q0 + BM + off);
   const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
@@ -100,16 +94,25 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
 
   // Direct global -> LDS tile load: wave w issues LDI 1 KB chunks; lane t of
   // chunk c lands at tile byte (w*LDI + c)*1024 + 16t = (row, swizzled seg).
-  auto tile_load = [&](const __amdgpu_buffer_rsrc_t& rs, int64_t sn, int j, int buf) {
+  // The buffer descriptor is rebuilt per tile (scalar work) and clipped to
+  // the rows that exist, so the per-lane byte offsets are loop-invariant and
+  // rows at or past nk read as zero.
+  int kvo[LDI], vvo[LDI];
+#pragma unroll
+  for (int c = 0; c < LDI; ++c) {
+    const int byte = (wave * LDI + c) * 1024 + lane * 16;
+    const int row = byte / (DP * 2);
+    const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+    kvo[c] = (int)(row * p.skn * 2) + seg * 16;
+    vvo[c] = (int)(row * p.svn * 2) + seg * 16;
+  }
+  auto tile_load = [&](const T* base, int64_t sn, const int* vo, int j, int buf) {
+    const int rows = min(nk - j * BN, BN);
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base + (int64_t)j * BN * sn, (int)(rows * sn * 2));
     LDS_AS char* dst = (LDS_AS char*)(smem + buf * TILE);
 #pragma unroll
-    for (int c = 0; c < LDI; ++c) {
-      const int byte = (wave * LDI + c) * 1024 + lane * 16;
-      const int row = byte / (DP * 2);
-      const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
-      const int voff = (int)(((int64_t)(j * BN + row) * sn + seg * 8) * 2);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(dst + (wave * LDI + c) * 1024), 16, voff, 0, 0, 0);
-    }
+    for (int c = 0; c < LDI; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(dst + (wave * LDI + c) * 1024), 16, vo[c], 0, 0, 0);
   };
 
   // Per-lane LDS byte offsets relative to a tile base. The swizzle depends
@@ -169,16 +172,16 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   };
 
   if (ntiles > 0) {
-    tile_load(krs, p.skn, 0, 0);
-    tile_load(vrs, p.svn, 0, 2);
+    tile_load(K, p.skn, kvo, 0, 0);
+    tile_load(V, p.svn, vvo, 0, 2);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
   for (int j = 0; j < ntiles; ++j) {
     if (j + 1 < ntiles) {
-      tile_load(krs, p.skn, j + 1, (j + 1) & 1);
-      tile_load(vrs, p.svn, j + 1, 2 + ((j + 1) & 1));
+      tile_load(K, p.skn, kvo, j + 1, (j + 1) & 1);
+      tile_load(V, p.svn, vvo, j + 1, 2 + ((j + 1) & 1));
     }
     const int kbase = j * BN;
     const bool active = !CAUSAL || (kbase <= qw_lo + 31 + off);
