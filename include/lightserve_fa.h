@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define LSFA_ABI_VERSION 1
+#define LSFA_ABI_VERSION 2
 
 typedef enum {
   LSFA_DTYPE_FP32 = 0,
@@ -85,11 +85,15 @@ typedef struct {
   int32_t reserved;
 } lsfa_fwd_args;
 
-/* Backward arguments. delta is a caller-allocated fp32 workspace shaped like
- * lse (rowsum(dO * O), kernels/flash_attention_backward.py:202-229); the
- * library writes it before using it. dq/dk/dv are written in the input dtype
- * (no fp32 dq staging buffer and no atomics: dq is produced by its own
- * query-stationary kernel, so results are deterministic). */
+/* Backward arguments. workspace is caller-allocated device memory of at
+ * least lsfa_bwd_workspace_size() bytes, 256-byte aligned; its contents on
+ * entry do not matter and are scratch afterwards. The library's prep pass
+ * writes there what the reference's preprocess kernel computes (delta =
+ * rowsum(dO * O), kernels/flash_attention_backward.py:202-229) plus
+ * transposed copies of q and dout for the key-stationary kernel. dq/dk/dv
+ * are written in the input dtype (no fp32 dq staging buffer and no atomics:
+ * dq is produced by its own query-stationary kernel, so results are
+ * deterministic). */
 typedef struct {
   const void* q;
   const void* k;
@@ -100,7 +104,8 @@ typedef struct {
   void* dq;
   void* dk;
   void* dv;
-  float* delta;
+  void* workspace;
+  uint64_t workspace_bytes;
   int64_t q_stride[4];
   int64_t k_stride[4];
   int64_t v_stride[4];
@@ -109,7 +114,7 @@ typedef struct {
   int64_t dq_stride[4];
   int64_t dk_stride[4];
   int64_t dv_stride[4];
-  int64_t lse_stride[3];       /* shared by lse and delta */
+  int64_t lse_stride[3];
   const int32_t* cu_seqlens_q; /* must be NULL: varlen backward is not implemented */
   const int32_t* cu_seqlens_k;
   int32_t dtype;
@@ -143,6 +148,10 @@ int lsfa_fwd(const lsfa_fwd_args* args, void* stream);
 
 /* Host-only validation of backward arguments; never touches the GPU. */
 int lsfa_bwd_check(const lsfa_bwd_args* args);
+
+/* Workspace bytes lsfa_bwd needs for these arguments (only dtype, batch,
+ * heads_q, seqlen_q and head_dim matter); no GPU work. */
+int lsfa_bwd_workspace_size(const lsfa_bwd_args* args, uint64_t* bytes);
 
 /* Backward: delta, then dq, dk, dv. Replaces the preprocess launch
  * (kernels/flash_attention_backward.py:341-350), the backward launch

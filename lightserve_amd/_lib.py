@@ -13,7 +13,7 @@ import torch
 
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
 TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}
@@ -21,7 +21,7 @@ TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfl
 STATUS = {0: "LSFA_OK", -1: "LSFA_ERR_INVALID", -2: "LSFA_ERR_UNSUPPORTED", -3: "LSFA_ERR_LAUNCH"}
 
 EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "lsfa_fwd",
-                    "lsfa_bwd_check", "lsfa_bwd")
+                    "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd")
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -48,7 +48,7 @@ class BwdArgs(ctypes.Structure):
         ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
         ("o", ctypes.c_void_p), ("dout", ctypes.c_void_p), ("lse", ctypes.c_void_p),
         ("dq", ctypes.c_void_p), ("dk", ctypes.c_void_p), ("dv", ctypes.c_void_p),
-        ("delta", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64),
         ("q_stride", _i64x4), ("k_stride", _i64x4), ("v_stride", _i64x4), ("o_stride", _i64x4),
         ("do_stride", _i64x4), ("dq_stride", _i64x4), ("dk_stride", _i64x4), ("dv_stride", _i64x4),
         ("lse_stride", _i64x3),
@@ -93,6 +93,8 @@ def load():
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
+        lib.lsfa_bwd_workspace_size.restype = ctypes.c_int
+        lib.lsfa_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdArgs), ctypes.POINTER(ctypes.c_uint64)]
         version = lib.lsfa_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"{_LIB_NAME} has ABI version {version}, expected {ABI_VERSION}")
@@ -117,6 +119,13 @@ def bwd_check(args):
     lib = load()
     rc = lib.lsfa_bwd_check(ctypes.byref(args))
     return rc, lib.lsfa_last_error().decode(errors="replace")
+
+
+def bwd_workspace_size(args):
+    """Bytes of device workspace lsfa_bwd needs for these arguments (host only)."""
+    n = ctypes.c_uint64(0)
+    _raise_on(load().lsfa_bwd_workspace_size(ctypes.byref(args), ctypes.byref(n)), "lsfa_bwd_workspace_size")
+    return n.value
 
 
 def fwd(args, stream):

@@ -70,6 +70,32 @@ int check_common(int dtype, int batch, int hq, int hkv, int nq, int nk, int d, f
   return LSFA_OK;
 }
 
+// Backward workspace: (lse*log2e, delta) pairs for every (b, h, query) and,
+// on the bf16/fp16 path, transposed copies of Q and dO. Queries are padded to
+// a multiple of the key-stationary query tile (64); each part starts on a
+// 256-byte boundary.
+struct BwdWorkspace {
+  int64_t nq_pad = 0;
+  uint64_t ld_off = 0, qt_off = 0, dot_off = 0, bytes = 0;
+};
+
+uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
+
+BwdWorkspace bwd_workspace(int dtype, int batch, int heads, int nq, int head_dim) {
+  BwdWorkspace w;
+  w.nq_pad = ((int64_t)nq + 63) / 64 * 64;
+  const uint64_t rows = (uint64_t)batch * heads * w.nq_pad;
+  w.ld_off = 0;
+  w.bytes = align256(rows * 8);
+  if (dtype != LSFA_DTYPE_FP32) {
+    const uint64_t tb = align256(rows * padded_dim(head_dim) * 2);
+    w.qt_off = w.bytes;
+    w.dot_off = w.bytes + tb;
+    w.bytes += 2 * tb;
+  }
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
@@ -145,8 +171,15 @@ int lsfa_bwd_check(const lsfa_bwd_args* a) {
   if (a->heads_kv != a->heads_q) return fail(LSFA_ERR_UNSUPPORTED, "GQA backward is not implemented (heads_kv != heads_q)");
   const bool empty = (long long)a->batch * a->heads_q * (a->seqlen_q + a->seqlen_k) == 0;
   if (!empty) {
-    if (!a->q || !a->k || !a->v || !a->o || !a->dout || !a->lse || !a->dq || !a->dk || !a->dv || !a->delta)
-      return fail(LSFA_ERR_INVALID, "q, k, v, o, dout, lse, dq, dk, dv and delta must be non-NULL");
+    if (!a->q || !a->k || !a->v || !a->o || !a->dout || !a->lse || !a->dq || !a->dk || !a->dv)
+      return fail(LSFA_ERR_INVALID, "q, k, v, o, dout, lse, dq, dk and dv must be non-NULL");
+    const BwdWorkspace w = bwd_workspace(a->dtype, a->batch, a->heads_q, a->seqlen_q, a->head_dim);
+    if (w.bytes > 0 && !a->workspace) return fail(LSFA_ERR_INVALID, "workspace must be non-NULL");
+    if (a->workspace_bytes < w.bytes)
+      return fail(LSFA_ERR_INVALID, "workspace_bytes %llu is below the %llu bytes lsfa_bwd_workspace_size asks for",
+                  (unsigned long long)a->workspace_bytes, (unsigned long long)w.bytes);
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
+      return fail(LSFA_ERR_INVALID, "workspace is not 256-byte aligned");
     if (a->dtype != LSFA_DTYPE_FP32) {
       if (a->head_dim % 8 != 0)
         return fail(LSFA_ERR_UNSUPPORTED, "bf16/fp16 head_dim must be a multiple of 8 (got %d)", a->head_dim);
@@ -161,6 +194,14 @@ int lsfa_bwd_check(const lsfa_bwd_args* a) {
   return ok();
 }
 
+int lsfa_bwd_workspace_size(const lsfa_bwd_args* a, uint64_t* bytes) {
+  if (a == nullptr || bytes == nullptr) return fail(LSFA_ERR_INVALID, "args or bytes is NULL");
+  int rc = check_common(a->dtype, a->batch, a->heads_q, a->heads_kv, a->seqlen_q, a->seqlen_k, a->head_dim, a->sm_scale);
+  if (rc) return rc;
+  *bytes = bwd_workspace(a->dtype, a->batch, a->heads_q, a->seqlen_q, a->head_dim).bytes;
+  return ok();
+}
+
 int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
   int rc = lsfa_bwd_check(a);
   if (rc) return rc;
@@ -168,7 +209,19 @@ int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
   lsfa::BwdParams p;
   memset(&p, 0, sizeof(p));
   p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.dout = a->dout; p.lse = a->lse;
-  p.dq = a->dq; p.dk = a->dk; p.dv = a->dv; p.delta = a->delta;
+  p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
+  const BwdWorkspace w = bwd_workspace(a->dtype, a->batch, a->heads_q, a->seqlen_q, a->head_dim);
+  char* ws = static_cast<char*>(a->workspace);
+  p.nq_pad = (int)w.nq_pad;
+  p.ld = reinterpret_cast<float*>(ws + w.ld_off);
+  p.sldh = 2 * w.nq_pad;
+  p.sldb = (int64_t)a->heads_q * p.sldh;
+  if (a->dtype != LSFA_DTYPE_FP32) {
+    p.qt = ws + w.qt_off;
+    p.dot = ws + w.dot_off;
+    p.sth = (int64_t)padded_dim(a->head_dim) * w.nq_pad;
+    p.stb = (int64_t)a->heads_q * p.sth;
+  }
   p.sqb = a->q_stride[0]; p.sqh = a->q_stride[1]; p.sqn = a->q_stride[2]; p.sqd = a->q_stride[3];
   p.skb = a->k_stride[0]; p.skh = a->k_stride[1]; p.skn = a->k_stride[2]; p.skd = a->k_stride[3];
   p.svb = a->v_stride[0]; p.svh = a->v_stride[1]; p.svn = a->v_stride[2]; p.svd = a->v_stride[3];

@@ -10,20 +10,98 @@
 //
 // Unlike the reference (one key-stationary kernel with fp32 atomic adds into
 // a dq workspace, :323-325, followed by a cast, :382), the work is split into
-//   fa_bwd_dq_kernel   : query-stationary; computes delta for its rows, then
-//                        dQ = scale * dS K over all visible key tiles, stored
-//                        straight in the input dtype;
+//   fa_bwd_prep_kernel : per query row, L*log2(e) and delta into the
+//                        workspace, plus transposed copies of Q and dO whose
+//                        query order matches the MFMA register layout of P
+//                        and dS (replaces the preprocess launch, :341-350);
+//   fa_bwd_dq_kernel   : query-stationary; dQ = scale * dS K over all visible
+//                        key tiles, stored straight in the input dtype;
 //   fa_bwd_dkdv_kernel : key-stationary; dK, dV over all visible query tiles.
-// Both recompute S and dP. There are no atomics and no fp32 dq buffer, so the
-// result is deterministic; the dq kernel must run first (it writes delta).
+// Both main kernels recompute S and dP. There are no atomics and no fp32 dq
+// buffer, so results are deterministic.
 #include "fa_common.hpp"
 
 namespace lsfa {
 
 constexpr float kLog2eB = 1.4426950408889634f;
 
+// Stored position of tile-local query q in a transposed Q/dO row (and the
+// query held at stored position q: bits 2 and 3 swap, an involution). The 8
+// queries one lane half feeds to a 32x32x16 MFMA from P or dS,
+// 16*ks + 8*(s/4) + 4*half + s%4 for s = 0..7, then sit in 16 contiguous bytes.
+__device__ __forceinline__ int tpos(int q) { return (q & ~12) | ((q & 4) << 1) | ((q & 8) >> 1); }
+
+// 16-byte column swizzle of a transposed [DP][64] tile (128-byte rows): any
+// 16 consecutive rows read at one logical column hit distinct bank groups.
+__device__ __forceinline__ int tswz(int d) { return (d & 7) ^ ((d >> 3) & 1); }
+
 // ---------------------------------------------------------------------------
-// dQ (and delta). Workgroup = 4 waves x 32 query rows, at most 256 registers
+// Prep: one workgroup per 64 query rows of one (b, h); four threads per row.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void fa_bwd_prep_kernel(const BwdParams p) {
+  using X8 = typename VecT<T>::x8;
+  constexpr int BM = 64, CPT = DP / 4, LDW = DP + 8;
+  __shared__ __attribute__((aligned(16))) T qs[BM * LDW];
+  __shared__ __attribute__((aligned(16))) T dos[BM * LDW];
+  const int tid = threadIdx.x, r = tid >> 2, part = tid & 3;
+  const int bh = blockIdx.y, b = bh / p.H, h = bh - b * p.H;
+  const int q0 = blockIdx.x * BM, q = q0 + r;
+  const bool valid = q < p.Nq;
+  const int D = p.D;
+  const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
+  const T* Og = (const T*)p.o + (int64_t)b * p.sob + (int64_t)h * p.soh;
+  const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
+
+  float dsum = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPT; c += 8) {
+    const int col = part * CPT + c;
+    u32x4 rq = {0, 0, 0, 0}, rd = {0, 0, 0, 0}, ro = {0, 0, 0, 0};
+    if (valid && col < D) {
+      rq = ldg16(Q + (int64_t)q * p.sqn + col);
+      rd = ldg16(dO + (int64_t)q * p.sdon + col);
+      ro = ldg16(Og + (int64_t)q * p.son + col);
+    }
+    const X8 dv = __builtin_bit_cast(X8, rd), ov = __builtin_bit_cast(X8, ro);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) dsum += (float)dv[s] * (float)ov[s];
+    *(u32x4*)&qs[r * LDW + col] = rq;
+    *(u32x4*)&dos[r * LDW + col] = rd;
+  }
+  dsum += __shfl_xor(dsum, 1);
+  dsum += __shfl_xor(dsum, 2);
+  if (part == 0) {
+    float l2 = INFINITY;  // no visible key, or padding row: P == 0
+    if (valid) {
+      const float L = p.lse[(int64_t)b * p.slb + (int64_t)h * p.slh + (int64_t)q * p.sln];
+      if (L != -INFINITY) l2 = L * kLog2eB;
+    }
+    float2 v;
+    v.x = l2;
+    v.y = valid ? dsum : 0.f;
+    *(float2*)(p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 2 * (int64_t)q) = v;
+  }
+  __syncthreads();
+
+  T* Qt = (T*)p.qt + (int64_t)b * p.stb + (int64_t)h * p.sth + q0;
+  T* dOt = (T*)p.dot + (int64_t)b * p.stb + (int64_t)h * p.sth + q0;
+  for (int u = tid; u < DP * 8; u += 256) {
+    const int d = u >> 3, sg = u & 7;
+    X8 vq, vd;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int src = tpos(sg * 8 + s);
+      vq[s] = qs[src * LDW + d];
+      vd[s] = dos[src * LDW + d];
+    }
+    *(X8*)(Qt + (int64_t)d * p.nq_pad + sg * 8) = vq;
+    *(X8*)(dOt + (int64_t)d * p.nq_pad + sg * 8) = vd;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ. Workgroup = 4 waves x 32 query rows, at most 256 registers
 // per wave so two workgroups share a CU. K/V tiles of 64 keys go global ->
 // LDS with buffer_load ... lds (double-buffered, zero past the sequence end).
 // Per key tile and wave:
@@ -60,38 +138,32 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
   const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh;
   const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh;
-  const T* Og = (const T*)p.o + (int64_t)b * p.sob + (int64_t)h * p.soh;
   const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
   T* dQ = (T*)p.dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh;
-  const float* Lg = p.lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
-  float* Dg = p.delta + (int64_t)b * p.slb + (int64_t)h * p.slh;
+  const float* LD = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh;
 
   const int qw_lo = q0 + wave * 32;
   const int qrow = qw_lo + l32;
   const bool qvalid = qrow < nq;
 
   X8 qreg[KSTEPS], doreg[KSTEPS];
-  float dpart = 0.f;
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
     const int col = 16 * kk + 8 * hh;
-    u32x4 rq = {0, 0, 0, 0}, rd = {0, 0, 0, 0}, ro = {0, 0, 0, 0};
+    u32x4 rq = {0, 0, 0, 0}, rd = {0, 0, 0, 0};
     if (qvalid && col < D) {
       rq = ldg16(Q + (int64_t)qrow * p.sqn + col);
       rd = ldg16(dO + (int64_t)qrow * p.sdon + col);
-      ro = ldg16(Og + (int64_t)qrow * p.son + col);
     }
     qreg[kk] = __builtin_bit_cast(X8, rq);
     doreg[kk] = __builtin_bit_cast(X8, rd);
-    const X8 ov = __builtin_bit_cast(X8, ro);
-#pragma unroll
-    for (int s = 0; s < 8; ++s) dpart += (float)doreg[kk][s] * (float)ov[s];
   }
-  const float delta = half_sum(dpart);
-  float lrow = qvalid ? Lg[(int64_t)qrow * p.sln] : INFINITY;
-  if (lrow == -INFINITY) lrow = INFINITY;  // row saw no key: P == 0
-  const float l2 = lrow * kLog2eB;
-  if (qvalid && hh == 0) Dg[(int64_t)qrow * p.sln] = delta;
+  float l2 = INFINITY, delta = 0.f;
+  if (qvalid) {
+    const float2 v = *(const float2*)(LD + 2 * qrow);
+    l2 = v.x;
+    delta = v.y;
+  }
 
   int kv_end = nk;
   if (CAUSAL) kv_end = min(nk, q0 + BM + off);
@@ -219,151 +291,136 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 
 // ---------------------------------------------------------------------------
 // dK, dV. Workgroup = 8 waves (two per SIMD, at most 256 registers each)
-// over 128 keys. K and V of those keys stay in LDS for the whole kernel.
-// Query tiles of 64 rows are staged in LDS twice: row-major (A operand of
-// S = Q K^T and dP = dO V^T) and transposed with the row order permuted so
-// that each MFMA operand of dV^T += dO^T P and dK^T += Q^T dS is a single
-// ds_read_b128 (no transpose reads in the loop). Wave w owns keys
-// 32*(w%4)..+31 and query rows 32*(w/4)..+31 of every tile:
+// over 128 keys; K and V of those keys stay in LDS for the whole kernel.
+// Every operand reaches LDS with buffer_load ... lds (no register staging):
+// per 64-query tile, the row-major Q/dO tile (with L*log2e and delta) and
+// the transposed Q^T/dO^T tile from the prep workspace. The two halves are
+// prefetched in alternation: the transposed tile streams in while S and dP
+// are computed, the next row tile while dV and dK accumulate. Wave w owns
+// keys 32*(w%4)..+31 and query rows 32*(w/4)..+31 of every tile:
 //   S  = Q K^T            A = Q rows (LDS),   B = K rows (LDS)
 //   dP = dO V^T           A = dO rows (LDS),  B = V rows (LDS)
 //   P  = exp2(S*scale*log2e - L*log2e), dS = P (dP - delta)
 //   dV^T += dO^T P        A = dO^T (LDS),     B = P  (registers)
 //   dK^T += Q^T dS        A = Q^T (LDS),      B = dS (registers)
 // The two query halves' partial dK/dV are summed through LDS at the end.
-// Query rows beyond the sequence get L = +inf, so their P is exactly 0.
+// Query rows beyond the sequence have L = +inf in the workspace, so their P
+// is exactly 0; head-dim columns at or past D load as zero.
 // ---------------------------------------------------------------------------
-
-// Position of tile-local query q (0..63) in a transposed tile row: bits 2
-// and 3 swap, so that the 8 queries one lane half feeds to a 32x32x16 MFMA
-// (16*kk + 8*(s/4) + 4*h + s%4, s = 0..7) sit in 16 contiguous bytes.
-__device__ __forceinline__ int tpos(int q) { return (q & ~12) | ((q & 4) << 1) | ((q & 8) >> 1); }
-// Byte offset of (row d, position pos) in a transposed [DP][64] tile; the
-// 16-byte column is XOR-swizzled with (d/2)%8 so 16 consecutive rows read
-// at one column hit distinct banks.
-__device__ __forceinline__ int toff(int d, int pos) { return d * 128 + ((((pos >> 3) ^ ((d >> 1) & 7))) << 4) + (pos & 7) * 2; }
-
 template <typename T, int DP, bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
+  using X4 = typename VecT<T>::x4;
   constexpr int NW = 8, BNK = 128, BMQ = 64;
-  constexpr int SEGS = DP / 8;
-  constexpr int KSTEPS = DP / 16;
-  constexpr int DT = DP / 32;
-  constexpr int KV_BYTES = BNK * DP * 2;               // one of K or V
-  constexpr int QT_BYTES = BMQ * DP * 2;               // one Q-side tile (any layout)
-  constexpr int UNITS = (BMQ / 4) * SEGS;              // 4-row x 8-column units per tensor
-  constexpr int LDI = KV_BYTES / 1024 / NW;            // direct 1 KB loads per wave for K or V
-  static_assert(LDI >= 1 && UNITS <= 256, "tile shape");
-  // LDS: K | V | Qr | dOr | Qt | dOt | L | delta
-  constexpr int OFF_K = 0, OFF_V = KV_BYTES, OFF_QR = 2 * KV_BYTES, OFF_OR = OFF_QR + QT_BYTES;
-  constexpr int OFF_QT = OFF_OR + QT_BYTES, OFF_OT = OFF_QT + QT_BYTES, OFF_L = OFF_OT + QT_BYTES;
-  constexpr int LDS_BYTES = OFF_L + 2 * BMQ * 4;
-  __shared__ __attribute__((aligned(1024))) char smem_raw[LDS_BYTES];
-  LDS_AS char* sm = (LDS_AS char*)smem_raw;
+  constexpr int KSTEPS = DP / 16, DT = DP / 32;
+  constexpr int KV_B = BNK * DP * 2;  // bytes of K (or V)
+  constexpr int R_B = BMQ * DP * 2;   // bytes of a row-major Q (or dO) tile
+  constexpr int T_B = DP * BMQ * 2;   // bytes of a transposed Q (or dO) tile
+  constexpr int OFF_K = 0, OFF_V = KV_B, OFF_Q = 2 * KV_B, OFF_DO = OFF_Q + R_B;
+  constexpr int OFF_QT = OFF_DO + R_B, OFF_DOT = OFF_QT + T_B, OFF_LD = OFF_DOT + T_B;
+  constexpr int LDS_B = OFF_LD + BMQ * 8;
+  constexpr int NG = 2 * DT * 4;  // f32x4 groups of dK^T and dV^T per lane
+  static_assert((NW / 2) * NG * 64 * 16 <= LDS_B, "epilogue does not fit in LDS");
+  constexpr int CKV = 2 * KV_B / 1024 / NW;  // 1 KB chunks per wave: K|V
+  constexpr int CR = 2 * R_B / 1024 / NW;    //                        Q|dO rows
+  constexpr int CT = 2 * T_B / 1024 / NW;    //                        Q^T|dO^T
+  static_assert(CKV >= 1 && CR >= 1 && CT >= 1, "tile too small for the workgroup");
+
+  __shared__ __attribute__((aligned(1024))) char sm_raw[LDS_B];
+  LDS_AS char* sm = (LDS_AS char*)sm_raw;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
-  const int kbw = wave & 3, qh = wave >> 2;  // key block and query half of this wave
+  const int kb = wave & 3, qh = wave >> 2;
+  const bool w_hi = wave >= NW / 2;  // waves 4..7 load V, dO, dO^T; 0..3 load K, Q, Q^T
   int bh, kt;
-  map_tile(p.num_tiles, gridDim.x, bh, kt, false);
+  map_tile(p.num_tiles, gridDim.x, bh, kt, false);  // low key tiles see the most queries
   const int b = bh / p.H, h = bh - b * p.H;
   const int nq = p.Nq, nk = p.Nk, D = p.D;
   const int k0 = kt * BNK;
   const int off = nk - nq;
 
-  const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
   const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh + (int64_t)k0 * p.skn;
   const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh + (int64_t)k0 * p.svn;
+  const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
   const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
-  T* dK = (T*)p.dk + (int64_t)b * p.sdkb + (int64_t)h * p.sdkh;
-  T* dV = (T*)p.dv + (int64_t)b * p.sdvb + (int64_t)h * p.sdvh;
-  const float* Lg = p.lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
-  const float* Dg = p.delta + (int64_t)b * p.slb + (int64_t)h * p.slh;
+  const T* Qt = (const T*)p.qt + (int64_t)b * p.stb + (int64_t)h * p.sth;
+  const T* dOt = (const T*)p.dot + (int64_t)b * p.stb + (int64_t)h * p.sth;
+  const float* LD = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh;
 
-  // K and V of the 128 keys: direct loads, zero past the sequence end.
+  // Lane byte offset of row-major chunk lc (tile rows of 2*DP bytes): lane t
+  // fills stored segment (byte % 2DP)/16, which holds logical segment
+  // stored ^ seg_swz(row). Logical columns at or past D get an offset past
+  // any descriptor's end, so they read as zero.
+  auto row_voff = [&](int lc, int64_t sn) -> int {
+    const int byte = lc * 1024 + lane * 16;
+    const int row = byte / (DP * 2);
+    const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+    return seg * 8 < D ? (int)(row * sn * 2) + seg * 16 : (int)0x80000000;
+  };
+
+  // K and V of the 128 keys (rows past nk read as zero).
   {
-    const int kn = max(0, min(BNK, nk - k0));
-    const __amdgpu_buffer_rsrc_t krs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, (int)((int64_t)kn * p.skn * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t vrs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, (int)((int64_t)kn * p.svn * 2), 0x00020000);
+    const int rows = max(0, min(BNK, nk - k0));
+    const int64_t sn = w_hi ? p.svn : p.skn;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(w_hi ? V : K, (int)(rows * sn * 2));
 #pragma unroll
-    for (int c = 0; c < LDI; ++c) {
-      const int byte = (wave * LDI + c) * 1024 + lane * 16;
-      const int row = byte / (DP * 2);
-      const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (LDS_AS void*)(sm + OFF_K + (wave * LDI + c) * 1024), 16,
-                                               (int)(((int64_t)row * p.skn + seg * 8) * 2), 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (LDS_AS void*)(sm + OFF_V + (wave * LDI + c) * 1024), 16,
-                                               (int)(((int64_t)row * p.svn + seg * 8) * 2), 0, 0, 0);
+    for (int i = 0; i < CKV; ++i) {
+      const int c = wave * CKV + i;  // chunk of the K|V region
+      const int vo = row_voff(c % (KV_B / 1024), sn);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(sm + OFF_K + c * 1024), 16, vo, 0, 0, 0);
     }
   }
 
-  // Query range that can see this key tile.
-  int q_lo = 0;
-  if (CAUSAL) q_lo = max(0, k0 - off);
-  q_lo = (q_lo / BMQ) * BMQ;
-  const int ntiles = (nq > q_lo) ? (nq - q_lo + BMQ - 1) / BMQ : 0;
+  int rvo[CR], tvo[CT];
+#pragma unroll
+  for (int i = 0; i < CR; ++i) rvo[i] = row_voff((wave % (NW / 2)) * CR + i, w_hi ? p.sdon : p.sqn);
+#pragma unroll
+  for (int i = 0; i < CT; ++i) {
+    const int byte = ((wave % (NW / 2)) * CT + i) * 1024 + lane * 16;
+    const int d = byte / (BMQ * 2);
+    const int seg = ((byte % (BMQ * 2)) / 16) ^ tswz(d);
+    tvo[i] = d * p.nq_pad * 2 + seg * 16;
+  }
 
-  // Staging: thread t < 2*UNITS loads one 4-row x 8-column unit of Q (t <
-  // UNITS) or dO; threads 0..15 also load 4 values of L, threads 16..31 of
-  // delta.
-  const bool is_do = tid >= UNITS;
-  const int u = is_do ? tid - UNITS : tid;
-  const bool stager = tid < 2 * UNITS;
-  const int g4 = u % (BMQ / 4), dseg = u / (BMQ / 4);
-  const T* src = is_do ? dO : Q;
-  const int64_t sstride = is_do ? p.sdon : p.sqn;
-  u32x4 st[4];
-  f32x4 lst = {0.f, 0.f, 0.f, 0.f};
-  const int lrow = tid;  // 0..15: L, 16..31: delta
-  auto gload = [&](int t) {
-    const int qs = q_lo + t * BMQ;
-    if (stager) {
+  // (Offset arrays go in as pointers and lambda results are hoisted into
+  // locals: an array-reference lambda parameter, or a lambda call inside a
+  // builtin's argument list, makes clang's host pass silently drop the
+  // kernel's launch stub.)
+  auto load_rows = [&](int t, const int* vo) {
+    const int q0 = t * BMQ;
+    const int rows = min(nq - q0, BMQ);
+    const int64_t sn = w_hi ? p.sdon : p.sqn;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc((w_hi ? dO : Q) + (int64_t)q0 * sn, (int)(rows * sn * 2));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int q = qs + 4 * g4 + r;
-        st[r] = (q < nq && dseg * 8 < D) ? ldg16(src + (int64_t)q * sstride + dseg * 8) : u32x4{0, 0, 0, 0};
-      }
-    }
-    if (lrow < 32) {
-      const int base = qs + 4 * (lrow & 15);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int q = base + e;
-        if (lrow < 16) {
-          float lv = q < nq ? Lg[(int64_t)q * p.sln] : INFINITY;
-          if (lv == -INFINITY) lv = INFINITY;  // row saw no key: P == 0
-          lst[e] = lv * 1.4426950408889634f;
-        } else {
-          lst[e] = q < nq ? Dg[(int64_t)q * p.sln] : 0.f;
-        }
-      }
+    for (int i = 0; i < CR; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(sm + OFF_Q + (wave * CR + i) * 1024), 16, vo[i],
+                                               0, 0, 0);
+    if (wave == 0 && lane < BMQ * 8 / 16) {
+      const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(LD + 2 * (int64_t)q0, BMQ * 8);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (LDS_AS void*)(sm + OFF_LD), 16, lane * 16, 0, 0, 0);
     }
   };
-  auto sstore = [&]() {
-    if (stager) {
-      const int qr = is_do ? OFF_OR : OFF_QR;
-      const int qt = is_do ? OFF_OT : OFF_QT;
+  auto load_trans = [&](int t, const int* vo) {
+    const T* base = (w_hi ? dOt : Qt) + t * BMQ;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base, (int)((int64_t)(DP - 1) * p.nq_pad * 2 + BMQ * 2));
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *(LDS_AS u32x4*)(sm + qr + swz_off<DP>(4 * g4 + r, dseg * 8) * 2) = st[r];
-      // Transposed: row d = 8*dseg + i holds the 4 queries' values of column i.
-      const int pos = tpos(4 * g4);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int w = i >> 1, sh = (i & 1) * 16;
-        const uint32_t lo = ((st[0][w] >> sh) & 0xffffu) | (((st[1][w] >> sh) & 0xffffu) << 16);
-        const uint32_t hi = ((st[2][w] >> sh) & 0xffffu) | (((st[3][w] >> sh) & 0xffffu) << 16);
-        *(LDS_AS u32x2*)(sm + qt + toff(dseg * 8 + i, pos)) = u32x2{lo, hi};
-      }
-    }
-    if (lrow < 32) {
-      *(LDS_AS f32x4*)(sm + OFF_L + lrow * 16) = lst;
-    }
+    for (int i = 0; i < CT; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(sm + OFF_QT + (wave * CT + i) * 1024), 16, vo[i],
+                                               0, 0, 0);
   };
+
+  // LDS read offsets. Row-major tiles: the swizzle depends on row & 15, so
+  // the wave's 32-row blocks are plain byte offsets. Transposed tiles: row
+  // d = 32*dt + l32, stored column (4*qh + 2*ks + hh) ^ tswz(l32).
+  int roff[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) roff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
+  const int qrow_b = 32 * qh * DP * 2, krow_b = 32 * kb * DP * 2;
+  int toffs[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) toffs[ks] = l32 * (BMQ * 2) + (((4 * qh + 2 * ks + hh) ^ tswz(l32)) << 4);
 
   f32x16 dk[DT], dv[DT];
 #pragma unroll
@@ -372,55 +429,42 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     dv[dt] = f32x16{};
   }
   const float sl2 = p.scale_log2;
-  const int krow = k0 + 32 * kbw + l32;  // key owned by this lane (C-layout column)
-  int aoff[KSTEPS];                      // Q/dO rows (A) and K/V rows (B): same swizzle
-#pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) aoff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
-  int toffs[DT][2];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int kk2 = 0; kk2 < 2; ++kk2) toffs[dt][kk2] = toff(32 * dt + l32, 32 * qh + 16 * kk2 + 8 * hh);
+  const int n_qt = p.nq_pad / BMQ;
+  int t_begin = 0;
+  if (CAUSAL) t_begin = max(0, k0 - off) / BMQ;  // first tile holding a query that sees key k0
+  const int kcol = k0 + 32 * kb + l32;            // this lane's key
 
-  if (ntiles > 0) gload(0);
-  for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();  // previous tile fully consumed (and K/V resident on t = 0)
-    sstore();
-    if (t == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t + 1 < ntiles) gload(t + 1);
-    const int qs = q_lo + t * BMQ;
-    const int qw = qs + 32 * qh;          // first query row of this wave
-    const int kw = k0 + 32 * kbw;         // first key of this wave
-    // Tiles where every key of the wave lies after every query row are not
-    // skipped: the causal mask zeroes their P and dS (they only occur among
-    // the first tiles of the sweep), which keeps the loop body branch-free
-    // apart from the mask itself.
+  if (t_begin < n_qt) load_rows(t_begin, rvo);
+  for (int t = t_begin; t < n_qt; ++t) {
+    const int q0 = t * BMQ;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // row tile t landed; everyone is done with the transposed tile t-1
+    load_trans(t, tvo);
+
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
-      const X8 aq = *(const LDS_AS X8*)(sm + OFF_QR + 32 * qh * DP * 2 + aoff[kk]);
-      const X8 ao = *(const LDS_AS X8*)(sm + OFF_OR + 32 * qh * DP * 2 + aoff[kk]);
-      const X8 bk = *(const LDS_AS X8*)(sm + OFF_K + 32 * kbw * DP * 2 + aoff[kk]);
-      const X8 bv = *(const LDS_AS X8*)(sm + OFF_V + 32 * kbw * DP * 2 + aoff[kk]);
-      s = mfma32(aq, bk, s);
-      dp = mfma32(ao, bv, dp);
+      s = mfma32(*(const LDS_AS X8*)(sm + OFF_Q + qrow_b + roff[kk]), *(const LDS_AS X8*)(sm + OFF_K + krow_b + roff[kk]), s);
+      dp = mfma32(*(const LDS_AS X8*)(sm + OFF_DO + qrow_b + roff[kk]), *(const LDS_AS X8*)(sm + OFF_V + krow_b + roff[kk]), dp);
     }
-    // Register 4g+e holds query qw + 8g + 4hh + e of this lane's key.
+    // Register i holds query q0 + 32*qh + 8*(i/4) + 4*hh + i%4 of key kcol;
+    // (L*log2e, delta) of those four consecutive queries are two 16-byte reads.
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int qi = 32 * qh + 8 * g + 4 * hh;
-      const f32x4 lv = *(const LDS_AS f32x4*)(sm + OFF_L + qi * 4);
-      const f32x4 dl = *(const LDS_AS f32x4*)(sm + OFF_L + BMQ * 4 + qi * 4);
+    for (int j = 0; j < 4; ++j) {
+      const LDS_AS f32x4* ldp = (const LDS_AS f32x4*)(sm + OFF_LD + (32 * qh + 8 * j + 4 * hh) * 8);
+      const f32x4 a = ldp[0], c = ldp[1];
+      const float l2v[4] = {a[0], a[2], c[0], c[2]};
+      const float dlv[4] = {a[1], a[3], c[1], c[3]};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float pv = fast_exp2(fmaf(s[4 * g + e], sl2, -lv[e]));
-        s[4 * g + e] = pv;
-        dp[4 * g + e] = pv * (dp[4 * g + e] - dl[e]);
+        const int i = 4 * j + e;
+        const float pv = fast_exp2(fmaf(s[i], sl2, -l2v[e]));
+        s[i] = pv;
+        dp[i] = pv * (dp[i] - dlv[e]);
       }
     }
-    if (CAUSAL && qw + off < kw + 31) {  // tile crosses the diagonal: drop keys after the query
-      const int lim = krow - off - qw - 4 * hh;  // masked if 8(i/4) + i%4 < lim
+    if (CAUSAL && k0 + 32 * kb + 31 > q0 + 32 * qh + off) {  // block crosses the diagonal
+      const int lim = kcol - (q0 + 32 * qh + 4 * hh + off);  // masked if 8*(i/4) + i%4 < lim
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const bool m = 8 * (i >> 2) + (i & 3) < lim;
@@ -428,77 +472,81 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
         dp[i] = m ? 0.f : dp[i];
       }
     }
-    const X8 pb0 = pack8<T>(s, 0), pb1 = pack8<T>(s, 8);
-    const X8 db0 = pack8<T>(dp, 0), db1 = pack8<T>(dp, 8);
+    const X8 P0 = pack8<T>(s, 0), P1 = pack8<T>(s, 8);
+    const X8 G0 = pack8<T>(dp, 0), G1 = pack8<T>(dp, 8);
+
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // transposed tile t landed; everyone is done with row tile t
+    if (t + 1 < n_qt) load_rows(t + 1, rvo);
+
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const X8 ao0 = *(const LDS_AS X8*)(sm + OFF_OT + toffs[dt][0]);
-      const X8 ao1 = *(const LDS_AS X8*)(sm + OFF_OT + toffs[dt][1]);
-      const X8 aq0 = *(const LDS_AS X8*)(sm + OFF_QT + toffs[dt][0]);
-      const X8 aq1 = *(const LDS_AS X8*)(sm + OFF_QT + toffs[dt][1]);
-      dv[dt] = mfma32(ao0, pb0, dv[dt]);
-      dk[dt] = mfma32(aq0, db0, dk[dt]);
-      dv[dt] = mfma32(ao1, pb1, dv[dt]);
-      dk[dt] = mfma32(aq1, db1, dk[dt]);
+      const int tb = dt * 32 * BMQ * 2;
+      dv[dt] = mfma32(*(const LDS_AS X8*)(sm + OFF_DOT + tb + toffs[0]), P0, dv[dt]);
+      dk[dt] = mfma32(*(const LDS_AS X8*)(sm + OFF_QT + tb + toffs[0]), G0, dk[dt]);
+      dv[dt] = mfma32(*(const LDS_AS X8*)(sm + OFF_DOT + tb + toffs[1]), P1, dv[dt]);
+      dk[dt] = mfma32(*(const LDS_AS X8*)(sm + OFF_QT + tb + toffs[1]), G1, dk[dt]);
     }
   }
 
-  // Sum the two query halves: waves 4..7 park their partials in LDS (over
-  // K/V, whose direct loads must have landed even if no tile ran).
+  // Sum the two query halves through LDS (f32x4 groups, lane-contiguous).
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  LDS_AS f32x4* park = (LDS_AS f32x4*)sm;  // (4 waves) x (2*DT*4) x 64 lanes x 16 B <= 128 KB
+  LDS_AS f32x4* park = (LDS_AS f32x4*)sm + kb * NG * 64 + lane;
   if (qh == 1) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        park[((kbw * 2 * DT + dt) * 4 + g) * 64 + lane] = f32x4{dk[dt][4 * g], dk[dt][4 * g + 1], dk[dt][4 * g + 2], dk[dt][4 * g + 3]};
-        park[(((kbw * 2 + 1) * DT + dt) * 4 + g) * 64 + lane] = f32x4{dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3]};
+        park[(dt * 4 + g) * 64] = f32x4{dk[dt][4 * g], dk[dt][4 * g + 1], dk[dt][4 * g + 2], dk[dt][4 * g + 3]};
+        park[(DT * 4 + dt * 4 + g) * 64] = f32x4{dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3]};
       }
   }
   __syncthreads();
-  if (qh == 0 && krow < nk) {
-    T* rk = dK + (int64_t)krow * p.sdkn;
-    T* rv = dV + (int64_t)krow * p.sdvn;
+  if (qh == 0 && kcol < nk) {
+    T* rk = (T*)p.dk + (int64_t)b * p.sdkb + (int64_t)h * p.sdkh + (int64_t)kcol * p.sdkn;
+    T* rv = (T*)p.dv + (int64_t)b * p.sdvb + (int64_t)h * p.sdvh + (int64_t)kcol * p.sdvn;
     const float sc = p.scale;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const f32x4 ok = park[((kbw * 2 * DT + dt) * 4 + g) * 64 + lane];
-        const f32x4 ov = park[(((kbw * 2 + 1) * DT + dt) * 4 + g) * 64 + lane];
         const int d = 32 * dt + 8 * g + 4 * hh;
         if (d < D) {
-          typename VecT<T>::x4 a, c;
+          const f32x4 ok = park[(dt * 4 + g) * 64];
+          const f32x4 ov = park[(DT * 4 + dt * 4 + g) * 64];
+          X4 ck, cv;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            a[e] = (T)((dk[dt][4 * g + e] + ok[e]) * sc);
-            c[e] = (T)(dv[dt][4 * g + e] + ov[e]);
+            ck[e] = (T)((dk[dt][4 * g + e] + ok[e]) * sc);
+            cv[e] = (T)(dv[dt][4 * g + e] + ov[e]);
           }
-          *(typename VecT<T>::x4*)(rk + d) = a;
-          *(typename VecT<T>::x4*)(rv + d) = c;
+          *(X4*)(rk + d) = ck;
+          *(X4*)(rv + d) = cv;
         }
       }
-    }
   }
 }
 
 template <typename T, int DP, bool CAUSAL>
 static hipError_t launch_bwd(BwdParams p, hipStream_t s) {
-  // An empty axis means an empty grid: that kernel has nothing to write.
-  p.num_tiles = (p.Nq + 127) / 128;
-  if (p.num_tiles > 0) {
+  // An empty axis means an empty grid: that kernel has nothing to write
+  // (with no queries dK = dV = 0 still needs the dK/dV kernel, which then
+  // runs no query tile).
+  hipError_t e = hipSuccess;
+  if (p.nq_pad > 0) {
+    hipLaunchKernelGGL((fa_bwd_prep_kernel<T, DP>), dim3(p.nq_pad / 64, p.B * p.H), dim3(256), 0, s, p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    p.num_tiles = (p.Nq + 127) / 128;
     hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(256), 0, s, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   p.num_tiles = (p.Nk + 127) / 128;
   if (p.num_tiles > 0) {
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(512), 0, s, p);
-    return hipGetLastError();
+    e = hipGetLastError();
   }
-  return hipSuccess;
+  return e;
 }
 
 template <typename T>

@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_f32_kernel(const BwdParams p, i
   const float* dO = (const float*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
   float* dQ = (float*)p.dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh;
   const float* Lg = p.lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
-  float* Dg = p.delta + (int64_t)b * p.slb + (int64_t)h * p.slh;
+  float* Dg = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 1;  // delta of query q at Dg[2q]
   const int qrow = q0 + qi;
   const bool valid = qrow < nq;
 
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_f32_kernel(const BwdParams p, i
   const float delta = quad_sum(dpart);
   float L = valid ? Lg[(int64_t)qrow * p.sln] : INFINITY;
   if (L == -INFINITY) L = INFINITY;
-  if (valid && part == 0) Dg[(int64_t)qrow * p.sln] = delta;
+  if (valid && part == 0) Dg[2 * (int64_t)qrow] = delta;
 
   int kv_end = nk;
   if (causal) kv_end = min(nk, q0 + RQ + off);
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_f32_kernel(const BwdParams p,
   float* dK = (float*)p.dk + (int64_t)b * p.sdkb + (int64_t)h * p.sdkh;
   float* dV = (float*)p.dv + (int64_t)b * p.sdvb + (int64_t)h * p.sdvh;
   const float* Lg = p.lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
-  const float* Dg = p.delta + (int64_t)b * p.slb + (int64_t)h * p.slh;
+  const float* Dg = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 1;  // delta of query q at Dg[2q]
   const int krow = k0 + ki;
   const bool valid = krow < nk;
 
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_f32_kernel(const BwdParams p,
       float lv = q < nq ? Lg[(int64_t)q * p.sln] : INFINITY;
       if (lv == -INFINITY) lv = INFINITY;
       Ls[tid] = lv;
-      Ds[tid] = q < nq ? Dg[(int64_t)q * p.sln] : 0.f;
+      Ds[tid] = q < nq ? Dg[2 * (int64_t)q] : 0.f;
     }
     __syncthreads();
 #pragma unroll 4

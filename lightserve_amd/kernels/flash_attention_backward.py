@@ -10,9 +10,10 @@ Drop-in for the reference's `kernels/flash_attention_backward.py`:
     assertions as the forward-only entry point.
 Keyword-only extra on every entry point: `sm_scale` (default 1/sqrt(D)).
 
-The backward recomputes P from L. delta = rowsum(dO * O) is produced inside
-the dQ kernel into a workspace allocated here, and dq/dk/dv come back in the
-input dtype from two deterministic kernels (no fp32 dq buffer, no atomics).
+The backward recomputes P from L. A prep kernel writes delta = rowsum(dO * O)
+(with L*log2(e) and transposed copies of q and dO) into a workspace allocated
+here, and dq/dk/dv come back in the input dtype from two deterministic
+kernels (no fp32 dq buffer, no atomics).
 """
 import torch
 
@@ -44,11 +45,11 @@ def _flash_attention_backward(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor
         outs.append(t if direct else torch.empty(B, H, N, dp, device=q.device, dtype=q.dtype))
     dqk, dkk, dvk = outs
     L = L.contiguous()
-    delta = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     assert L.shape == (B, H, N) and L.dtype == torch.float32, "L must be fp32 [B, H, N]"
     args = _lib.BwdArgs(
         q=qk.data_ptr(), k=kk.data_ptr(), v=vk.data_ptr(), o=ok_.data_ptr(), dout=dok.data_ptr(),
-        lse=L.data_ptr(), dq=dqk.data_ptr(), dk=dkk.data_ptr(), dv=dvk.data_ptr(), delta=delta.data_ptr(),
+        lse=L.data_ptr(), dq=dqk.data_ptr(), dk=dkk.data_ptr(), dv=dvk.data_ptr(), workspace=None,
+        workspace_bytes=0,
         q_stride=_lib.strides4(qk), k_stride=_lib.strides4(kk), v_stride=_lib.strides4(vk),
         o_stride=_lib.strides4(ok_), do_stride=_lib.strides4(dok), dq_stride=_lib.strides4(dqk),
         dk_stride=_lib.strides4(dkk), dv_stride=_lib.strides4(dvk), lse_stride=_lib._i64x3(*L.stride()),
@@ -56,6 +57,10 @@ def _flash_attention_backward(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor
         dtype=_lib.TORCH_TO_LSFA[q.dtype], batch=B, heads_q=H, heads_kv=H, seqlen_q=N, seqlen_k=N,
         head_dim=dp, causal=int(bool(causal)), sm_scale=scale, reserved=0,
     )
+    nbytes = _lib.bwd_workspace_size(args)
+    # The caching allocator hands out 512-byte aligned blocks (the ABI asks for 256).
+    workspace = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = workspace.data_ptr(), nbytes
     with torch.cuda.device(q.device):
         _lib.bwd(args, _lib.current_stream(q.device))
     for t, tk in ((dq, dqk), (dk, dkk), (dv, dvk)):

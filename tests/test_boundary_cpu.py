@@ -159,7 +159,8 @@ def test_abi_host_validation(built_library):
 
 def test_abi_backward_validation(built_library):
     st = _lib._i64x4(2048, 512, 64, 1)
-    args = _lib.BwdArgs(q=16, k=32, v=48, o=64, dout=80, lse=96, dq=112, dk=128, dv=144, delta=160,
+    args = _lib.BwdArgs(q=16, k=32, v=48, o=64, dout=80, lse=96, dq=112, dk=128, dv=144, workspace=4096,
+                        workspace_bytes=1 << 20,
                         q_stride=st, k_stride=st, v_stride=st, o_stride=st, do_stride=st, dq_stride=st,
                         dk_stride=st, dv_stride=st, lse_stride=_lib._i64x3(32, 8, 1),
                         cu_seqlens_q=None, cu_seqlens_k=None, dtype=_lib.DTYPE_BF16, batch=1,
@@ -170,11 +171,45 @@ def test_abi_backward_validation(built_library):
     rc, msg = _lib.bwd_check(args)
     assert rc == -2 and "GQA" in msg
     args.heads_kv = 4
-    args.delta = None
+    args.workspace = None
     rc, msg = _lib.bwd_check(args)
     assert rc == -1
-    args.delta = 160
+    args.workspace = 4096
     args.cu_seqlens_q = 16
     args.cu_seqlens_k = 32
     rc, msg = _lib.bwd_check(args)
     assert rc == -2 and "varlen" in msg
+    args.cu_seqlens_q = args.cu_seqlens_k = None
+
+
+def test_abi_backward_workspace(built_library):
+    """Workspace size: (L*log2e, delta) fp32 pairs for every (b, h, query) with
+    queries padded to 64, plus transposed bf16/fp16 copies of q and dout at the
+    padded head dim; each part 256-byte aligned. Too small or misaligned
+    workspaces are rejected before any launch."""
+    st = _lib._i64x4(2048, 512, 64, 1)
+    args = _lib.BwdArgs(q=16, k=32, v=48, o=64, dout=80, lse=96, dq=112, dk=128, dv=144, workspace=4096,
+                        workspace_bytes=0,
+                        q_stride=st, k_stride=st, v_stride=st, o_stride=st, do_stride=st, dq_stride=st,
+                        dk_stride=st, dv_stride=st, lse_stride=_lib._i64x3(32, 8, 1),
+                        cu_seqlens_q=None, cu_seqlens_k=None, dtype=_lib.DTYPE_BF16, batch=1,
+                        heads_q=4, heads_kv=4, seqlen_q=8, seqlen_k=8, head_dim=64, causal=1,
+                        sm_scale=0.125, reserved=0)
+    rows = 1 * 4 * 64
+    expected = rows * 8 + 2 * rows * 64 * 2
+    assert _lib.bwd_workspace_size(args) == expected
+    args.seqlen_q = 65  # two query tiles
+    assert _lib.bwd_workspace_size(args) == 2 * expected
+    args.seqlen_q = 8
+    args.workspace_bytes = expected - 1
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -1 and "workspace_bytes" in msg
+    args.workspace_bytes = expected
+    assert _lib.bwd_check(args)[0] == 0
+    args.workspace = 4096 + 128
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -1 and "aligned" in msg
+    args.workspace = 4096
+    # fp32 needs only the (L, delta) pairs
+    args.dtype = _lib.DTYPE_FP32
+    assert _lib.bwd_workspace_size(args) == rows * 8
