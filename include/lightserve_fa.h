@@ -87,7 +87,7 @@ typedef struct {
 
 /* Backward arguments. workspace is caller-allocated device memory of at
  * least lsfa_bwd_workspace_size() bytes, 256-byte aligned; its contents on
- * entry do not matter and are scratch afterwards. The library's prep pass
+ * entry do not matter and are scratch afterwards. The dq kernel's prologue
  * writes there what the reference's preprocess kernel computes (delta =
  * rowsum(dO * O), kernels/flash_attention_backward.py:202-229) plus
  * transposed copies of q and dout for the key-stationary kernel. dq/dk/dv

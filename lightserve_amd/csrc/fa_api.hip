@@ -72,8 +72,8 @@ int check_common(int dtype, int batch, int hq, int hkv, int nq, int nk, int d, f
 
 // Backward workspace: (lse*log2e, delta) pairs for every (b, h, query) and,
 // on the bf16/fp16 path, transposed copies of Q and dO. Queries are padded to
-// a multiple of the key-stationary query tile (64); each part starts on a
-// 256-byte boundary.
+// a multiple of the query-stationary tile (128, which the dq kernel writes
+// whole); each part starts on a 256-byte boundary.
 struct BwdWorkspace {
   int64_t nq_pad = 0;
   uint64_t ld_off = 0, qt_off = 0, dot_off = 0, bytes = 0;
@@ -83,7 +83,7 @@ uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
 BwdWorkspace bwd_workspace(int dtype, int batch, int heads, int nq, int head_dim) {
   BwdWorkspace w;
-  w.nq_pad = ((int64_t)nq + 63) / 64 * 64;
+  w.nq_pad = ((int64_t)nq + 127) / 128 * 128;
   const uint64_t rows = (uint64_t)batch * heads * w.nq_pad;
   w.ld_off = 0;
   w.bytes = align256(rows * 8);

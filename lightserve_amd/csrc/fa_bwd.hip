@@ -10,14 +10,15 @@
 //
 // Unlike the reference (one key-stationary kernel with fp32 atomic adds into
 // a dq workspace, :323-325, followed by a cast, :382), the work is split into
-//   fa_bwd_prep_kernel : per query row, L*log2(e) and delta into the
-//                        workspace, plus transposed copies of Q and dO whose
-//                        query order matches the MFMA register layout of P
-//                        and dS (replaces the preprocess launch, :341-350);
-//   fa_bwd_dq_kernel   : query-stationary; dQ = scale * dS K over all visible
-//                        key tiles, stored straight in the input dtype;
-//   fa_bwd_dkdv_kernel : key-stationary; dK, dV over all visible query tiles.
-// Both main kernels recompute S and dP. There are no atomics and no fp32 dq
+//   fa_bwd_dq_kernel   : query-stationary. Its prologue does the reference's
+//                        preprocess (:341-350): delta and L*log2(e) per query
+//                        row into the workspace, plus transposed copies of Q
+//                        and dO whose query order matches the MFMA register
+//                        layout of P and dS. Then dQ = scale * dS K over all
+//                        visible key tiles, stored straight in the input dtype;
+//   fa_bwd_dkdv_kernel : key-stationary; dK, dV over all visible query tiles
+//                        (runs after the dq kernel, which feeds it).
+// Both kernels recompute S and dP. There are no atomics and no fp32 dq
 // buffer, so results are deterministic.
 #include "fa_common.hpp"
 
@@ -34,71 +35,6 @@ __device__ __forceinline__ int tpos(int q) { return (q & ~12) | ((q & 4) << 1) |
 // 16-byte column swizzle of a transposed [DP][64] tile (128-byte rows): any
 // 16 consecutive rows read at one logical column hit distinct bank groups.
 __device__ __forceinline__ int tswz(int d) { return (d & 7) ^ ((d >> 3) & 1); }
-
-// ---------------------------------------------------------------------------
-// Prep: one workgroup per 64 query rows of one (b, h); four threads per row.
-// ---------------------------------------------------------------------------
-template <typename T, int DP>
-__global__ __launch_bounds__(256) void fa_bwd_prep_kernel(const BwdParams p) {
-  using X8 = typename VecT<T>::x8;
-  constexpr int BM = 64, CPT = DP / 4, LDW = DP + 8;
-  __shared__ __attribute__((aligned(16))) T qs[BM * LDW];
-  __shared__ __attribute__((aligned(16))) T dos[BM * LDW];
-  const int tid = threadIdx.x, r = tid >> 2, part = tid & 3;
-  const int bh = blockIdx.y, b = bh / p.H, h = bh - b * p.H;
-  const int q0 = blockIdx.x * BM, q = q0 + r;
-  const bool valid = q < p.Nq;
-  const int D = p.D;
-  const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
-  const T* Og = (const T*)p.o + (int64_t)b * p.sob + (int64_t)h * p.soh;
-  const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
-
-  float dsum = 0.f;
-#pragma unroll
-  for (int c = 0; c < CPT; c += 8) {
-    const int col = part * CPT + c;
-    u32x4 rq = {0, 0, 0, 0}, rd = {0, 0, 0, 0}, ro = {0, 0, 0, 0};
-    if (valid && col < D) {
-      rq = ldg16(Q + (int64_t)q * p.sqn + col);
-      rd = ldg16(dO + (int64_t)q * p.sdon + col);
-      ro = ldg16(Og + (int64_t)q * p.son + col);
-    }
-    const X8 dv = __builtin_bit_cast(X8, rd), ov = __builtin_bit_cast(X8, ro);
-#pragma unroll
-    for (int s = 0; s < 8; ++s) dsum += (float)dv[s] * (float)ov[s];
-    *(u32x4*)&qs[r * LDW + col] = rq;
-    *(u32x4*)&dos[r * LDW + col] = rd;
-  }
-  dsum += __shfl_xor(dsum, 1);
-  dsum += __shfl_xor(dsum, 2);
-  if (part == 0) {
-    float l2 = INFINITY;  // no visible key, or padding row: P == 0
-    if (valid) {
-      const float L = p.lse[(int64_t)b * p.slb + (int64_t)h * p.slh + (int64_t)q * p.sln];
-      if (L != -INFINITY) l2 = L * kLog2eB;
-    }
-    float2 v;
-    v.x = l2;
-    v.y = valid ? dsum : 0.f;
-    *(float2*)(p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 2 * (int64_t)q) = v;
-  }
-  __syncthreads();
-
-  T* Qt = (T*)p.qt + (int64_t)b * p.stb + (int64_t)h * p.sth + q0;
-  T* dOt = (T*)p.dot + (int64_t)b * p.stb + (int64_t)h * p.sth + q0;
-  for (int u = tid; u < DP * 8; u += 256) {
-    const int d = u >> 3, sg = u & 7;
-    X8 vq, vd;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int src = tpos(sg * 8 + s);
-      vq[s] = qs[src * LDW + d];
-      vd[s] = dos[src * LDW + d];
-    }
-    *(X8*)(Qt + (int64_t)d * p.nq_pad + sg * 8) = vq;
-    *(X8*)(dOt + (int64_t)d * p.nq_pad + sg * 8) = vd;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // dQ. Workgroup = 4 waves x 32 query rows, at most 256 registers
@@ -138,50 +74,124 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
   const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh;
   const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh;
+  const T* Og = (const T*)p.o + (int64_t)b * p.sob + (int64_t)h * p.soh;
   const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
   T* dQ = (T*)p.dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh;
-  const float* LD = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh;
 
   const int qw_lo = q0 + wave * 32;
   const int qrow = qw_lo + l32;
   const bool qvalid = qrow < nq;
 
-  X8 qreg[KSTEPS], doreg[KSTEPS];
+  // Lane byte offset of chunk lc of a row-major tile (rows of 2*DP bytes):
+  // lane t fills LDS bytes [16t, 16t+16) of the chunk, i.e. stored segment
+  // (byte % 2DP)/16 of a row, which holds logical segment stored ^
+  // seg_swz(row). Logical columns at or past D get an offset past any
+  // descriptor's end, so they read as zero.
+  auto row_voff = [&](int lc, int64_t sn) -> int {
+    const int byte = lc * 1024 + lane * 16;
+    const int row = byte / (DP * 2);
+    const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+    return seg * 8 < D ? (int)(row * sn * 2) + seg * 16 : (int)0x80000000;
+  };
+  const int tr_row = 4 * hh + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int troff[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    troff[dt][0] = swz_off<DP>(tr_row, 32 * dt + tr_col) * 2;
+    troff[dt][1] = swz_off<DP>(tr_row + 8, 32 * dt + tr_col) * 2;
+  }
+
+  // Prologue (the backward's per-query-row pass): the tile's Q and dO rows
+  // go to LDS (rows past nq and columns past D as zero), then
+  //   - Q^T and dO^T B operands of this kernel come from LDS;
+  //   - delta = rowsum(dO * O) and L*log2e are written to the workspace for
+  //     the dK/dV kernel;
+  //   - the transposed, query-permuted copies of Q and dO the dK/dV kernel
+  //     reads are written to the workspace. The transpose reads below return,
+  //     for lane (d = 32*dt + l32, hh) and query step ks, queries
+  //     16*ks + 8*(s/4) + 4*hh + s%4 (s = 0..7): stored positions
+  //     16*ks + 8*hh + s of the workspace layout.
+  constexpr int TB = BM * DP * 2;  // bytes of one 128-row tile
+  static_assert(2 * TB <= 4 * TILE * 2, "Q/dO tiles must fit in the K/V buffers");
+  {
+    constexpr int CPW = 2 * TB / 1024 / NW;  // chunks per wave (waves 0..1: Q, 2..3: dO)
+    const bool w_do = wave >= NW / 2;
+    const int64_t sn = w_do ? p.sdon : p.sqn;
+    const int rows = min(nq - q0, BM);
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc((w_do ? dO : Q) + (int64_t)q0 * sn, (int)(rows * sn * 2));
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const int c = wave * CPW + i;
+      const int vo = row_voff(c % (TB / 1024), sn);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(sm + c * 1024), 16, vo, 0, 0, 0);
+    }
+  }
+  u32x4 oraw[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
     const int col = 16 * kk + 8 * hh;
-    u32x4 rq = {0, 0, 0, 0}, rd = {0, 0, 0, 0};
-    if (qvalid && col < D) {
-      rq = ldg16(Q + (int64_t)qrow * p.sqn + col);
-      rd = ldg16(dO + (int64_t)qrow * p.sdon + col);
+    oraw[kk] = u32x4{0, 0, 0, 0};
+    if (qvalid && col < D) oraw[kk] = ldg16(Og + (int64_t)qrow * p.son + col);
+  }
+  float lraw = -INFINITY;
+  if (qvalid) lraw = p.lse[(int64_t)b * p.slb + (int64_t)h * p.slh + (int64_t)qrow * p.sln];
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  X8 qreg[KSTEPS], doreg[KSTEPS];
+  float dpart = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    const int o = swz_off<DP>(32 * wave + l32, 16 * kk + 8 * hh) * 2;
+    qreg[kk] = *(const LDS_AS X8*)(sm + o);
+    doreg[kk] = *(const LDS_AS X8*)(sm + TB + o);
+    const X8 ov = __builtin_bit_cast(X8, oraw[kk]);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) dpart += (float)doreg[kk][s] * (float)ov[s];
+  }
+  const float delta = half_sum(dpart);
+  const float l2 = lraw == -INFINITY ? INFINITY : lraw * kLog2eB;  // no visible key / padding: P == 0
+  if (hh == 0) {
+    float2 v;
+    v.x = l2;
+    v.y = delta;
+    *(float2*)(p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 2 * (int64_t)qrow) = v;
+  }
+  {
+    constexpr int KS = BM / 16, UNITS = 2 * DT * KS;
+    T* Qt = (T*)p.qt + (int64_t)b * p.stb + (int64_t)h * p.sth + q0 + 8 * hh;
+    T* dOt = (T*)p.dot + (int64_t)b * p.stb + (int64_t)h * p.sth + q0 + 8 * hh;
+#pragma unroll
+    for (int u0 = 0; u0 < UNITS; u0 += NW) {
+      const int u = u0 + wave;
+      const int tsel = u / (DT * KS), dt = (u / KS) % DT, ks = u % KS;
+      const LDS_AS char* base = sm + tsel * TB + ks * 16 * DP * 2;
+      int o0 = 0, o1 = 0;
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+        if (i == dt) {
+          o0 = troff[i][0];
+          o1 = troff[i][1];
+        }
+      const X8 a = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(base + o0)), lds_read_tr((const LDS_AS T*)(base + o1)));
+      *(X8*)((tsel ? dOt : Qt) + (int64_t)(32 * dt + l32) * p.nq_pad + 16 * ks) = a;
     }
-    qreg[kk] = __builtin_bit_cast(X8, rq);
-    doreg[kk] = __builtin_bit_cast(X8, rd);
   }
-  float l2 = INFINITY, delta = 0.f;
-  if (qvalid) {
-    const float2 v = *(const float2*)(LD + 2 * qrow);
-    l2 = v.x;
-    delta = v.y;
-  }
+  __syncthreads();  // the K/V tiles below reuse the Q/dO buffers
 
   int kv_end = nk;
   if (CAUSAL) kv_end = min(nk, q0 + BM + off);
   const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
-  // Direct tile loads: lane t of chunk c fills LDS bytes [16t, 16t+16) of
-  // that chunk, i.e. stored segment (byte % 2DP)/16 of a tile row, which holds
-  // logical segment stored ^ seg_swz(row). The buffer descriptor is rebuilt
-  // per tile (scalar work) and clipped to the rows that exist, so the
-  // per-lane byte offsets are loop-invariant and rows past nk read as zero.
+  // Direct tile loads of K and V (see row_voff). The buffer descriptor is
+  // rebuilt per tile (scalar work) and clipped to the rows that exist, so
+  // the per-lane byte offsets are loop-invariant and rows past nk read as zero.
   int kvo[LDI], vvo[LDI];
 #pragma unroll
   for (int c = 0; c < LDI; ++c) {
-    const int byte = (wave * LDI + c) * 1024 + lane * 16;
-    const int row = byte / (DP * 2);
-    const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
-    kvo[c] = (int)(row * p.skn * 2) + seg * 16;
-    vvo[c] = (int)(row * p.svn * 2) + seg * 16;
+    kvo[c] = row_voff(wave * LDI + c, p.skn);
+    vvo[c] = row_voff(wave * LDI + c, p.svn);
   }
   auto tile_load = [&](const T* base, int64_t sn, const int* vo, int j, int buf) {
     const int rows = min(nk - j * BN, BN);
@@ -195,14 +205,6 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   int koff[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) koff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
-  const int tr_row = 4 * hh + ((lane & 15) >> 2);
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  int troff[DT][2];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    troff[dt][0] = swz_off<DP>(tr_row, 32 * dt + tr_col) * 2;
-    troff[dt][1] = swz_off<DP>(tr_row + 8, 32 * dt + tr_col) * 2;
-  }
 
   f32x16 acc[DT];
 #pragma unroll
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 // over 128 keys; K and V of those keys stay in LDS for the whole kernel.
 // Every operand reaches LDS with buffer_load ... lds (no register staging):
 // per 64-query tile, the row-major Q/dO tile (with L*log2e and delta) and
-// the transposed Q^T/dO^T tile from the prep workspace. The two halves are
+// the transposed Q^T/dO^T tile from the workspace. The two halves are
 // prefetched in alternation: the transposed tile streams in while S and dP
 // are computed, the next row tile while dV and dK accumulate. Wave w owns
 // keys 32*(w%4)..+31 and query rows 32*(w/4)..+31 of every tile:
@@ -304,8 +306,9 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 //   dV^T += dO^T P        A = dO^T (LDS),     B = P  (registers)
 //   dK^T += Q^T dS        A = Q^T (LDS),      B = dS (registers)
 // The two query halves' partial dK/dV are summed through LDS at the end.
-// Query rows beyond the sequence have L = +inf in the workspace, so their P
-// is exactly 0; head-dim columns at or past D load as zero.
+// Query rows beyond the sequence have L = +inf in the workspace (written by
+// the dq kernel's prologue), so their P is exactly 0; head-dim columns at or
+// past D load as zero.
 // ---------------------------------------------------------------------------
 template <typename T, int DP, bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
@@ -429,7 +432,7 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     dv[dt] = f32x16{};
   }
   const float sl2 = p.scale_log2;
-  const int n_qt = p.nq_pad / BMQ;
+  const int n_qt = (nq + BMQ - 1) / BMQ;  // every tile starts below nq
   int t_begin = 0;
   if (CAUSAL) t_begin = max(0, k0 - off) / BMQ;  // first tile holding a query that sees key k0
   const int kcol = k0 + 32 * kb + l32;            // this lane's key
@@ -534,10 +537,8 @@ static hipError_t launch_bwd(BwdParams p, hipStream_t s) {
   // (with no queries dK = dV = 0 still needs the dK/dV kernel, which then
   // runs no query tile).
   hipError_t e = hipSuccess;
-  if (p.nq_pad > 0) {
-    hipLaunchKernelGGL((fa_bwd_prep_kernel<T, DP>), dim3(p.nq_pad / 64, p.B * p.H), dim3(256), 0, s, p);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    p.num_tiles = (p.Nq + 127) / 128;
+  p.num_tiles = (p.Nq + 127) / 128;
+  if (p.num_tiles > 0) {
     hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(256), 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }

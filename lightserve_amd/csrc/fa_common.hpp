@@ -148,7 +148,7 @@ struct BwdParams {
   void* dq;
   void* dk;
   void* dv;
-  // Workspace written by the backward's prep pass:
+  // Workspace written by the dq kernel's prologue:
   //   ld  : (lse * log2(e), delta) pairs, element (b, h, q) at b*sldb + h*sldh + 2q;
   //         +inf stands in for lse where a row sees no key or q >= Nq
   //   qt, dot : Q^T and dO^T in the input dtype (bf16/fp16 path only), element
@@ -158,7 +158,7 @@ struct BwdParams {
   void* qt;
   void* dot;
   int64_t sldb, sldh, stb, sth;
-  int nq_pad;  // Nq rounded up to the key-stationary query tile (64)
+  int nq_pad;  // Nq rounded up to the query-stationary tile (128)
   int64_t sqb, sqh, sqn;
   int64_t skb, skh, skn;
   int64_t svb, svh, svn;
@@ -192,11 +192,13 @@ __device__ __forceinline__ void map_tile(int num_tiles, int total, int& bh, int&
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *(const u32x4*)p; }
 
 // Raw buffer descriptor over [base, base + bytes): loads at or past the end
-// return zero. Callers pass wave-uniform values; readfirstlane keeps the size
-// in a scalar register even where the compiler computed it with VALU ops
-// (a vector descriptor would turn every load into a waterfall loop).
+// return zero, and a size below zero is taken as zero (every load returns
+// zero). Callers pass wave-uniform values; readfirstlane keeps the size in a
+// scalar register even where the compiler computed it with VALU ops (a
+// vector descriptor would turn every load into a waterfall loop).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+  const int n = __builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n > 0 ? n : 0, 0x00020000);
 }
 
 }  // namespace lsfa

@@ -10,9 +10,9 @@ Drop-in for the reference's `kernels/flash_attention_backward.py`:
     assertions as the forward-only entry point.
 Keyword-only extra on every entry point: `sm_scale` (default 1/sqrt(D)).
 
-The backward recomputes P from L. A prep kernel writes delta = rowsum(dO * O)
-(with L*log2(e) and transposed copies of q and dO) into a workspace allocated
-here, and dq/dk/dv come back in the input dtype from two deterministic
+The backward recomputes P from L. The dQ kernel's prologue writes
+delta = rowsum(dO * O) (with L*log2(e) and transposed copies of q and dO) into
+a workspace allocated here for the dK/dV kernel, and dq/dk/dv come back in the input dtype from two deterministic
 kernels (no fp32 dq buffer, no atomics).
 """
 import torch

@@ -184,7 +184,7 @@ def test_abi_backward_validation(built_library):
 
 def test_abi_backward_workspace(built_library):
     """Workspace size: (L*log2e, delta) fp32 pairs for every (b, h, query) with
-    queries padded to 64, plus transposed bf16/fp16 copies of q and dout at the
+    queries padded to 128, plus transposed bf16/fp16 copies of q and dout at the
     padded head dim; each part 256-byte aligned. Too small or misaligned
     workspaces are rejected before any launch."""
     st = _lib._i64x4(2048, 512, 64, 1)
@@ -195,10 +195,12 @@ def test_abi_backward_workspace(built_library):
                         cu_seqlens_q=None, cu_seqlens_k=None, dtype=_lib.DTYPE_BF16, batch=1,
                         heads_q=4, heads_kv=4, seqlen_q=8, seqlen_k=8, head_dim=64, causal=1,
                         sm_scale=0.125, reserved=0)
-    rows = 1 * 4 * 64
+    rows = 1 * 4 * 128
     expected = rows * 8 + 2 * rows * 64 * 2
     assert _lib.bwd_workspace_size(args) == expected
-    args.seqlen_q = 65  # two query tiles
+    args.seqlen_q = 128
+    assert _lib.bwd_workspace_size(args) == expected
+    args.seqlen_q = 129  # two query tiles
     assert _lib.bwd_workspace_size(args) == 2 * expected
     args.seqlen_q = 8
     args.workspace_bytes = expected - 1
