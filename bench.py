@@ -48,6 +48,9 @@ def parse_args():
     ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=2, help="heads in the CPU-baseline sample")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="before the warm-up, run 3 plain device copies of MIB MiB each (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters to bytes)")
     return ap.parse_args()
 
 
@@ -209,6 +212,15 @@ def main():
         o, lse = fwd()
         if bwd is not None:
             bwd(o, lse)
+
+    if args.calibrate_copy > 0:
+        # A plain copy of known size: reads and writes exactly MIB MiB each.
+        src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         step()

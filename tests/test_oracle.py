@@ -6,6 +6,7 @@ Checks, per oracle function:
   attention_grads      float64 gradcheck;
   flash_forward_tiled  (restated reference tile loop) vs attention_reference;
   flash_backward_tiled (restated reference backward) vs attention_grads;
+  bwd_delta            vs the identity delta_i = sum_j P_ij dP_ij;
   varlen_reference     vs pure-Python loops with GQA;
 and planted mistakes in copies of the oracle must fail these checks.
 """
@@ -17,8 +18,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from oracle.attention import (attention_grads, attention_reference, causal_mask, flash_backward_tiled,
-                              flash_forward_tiled, naive_attention, varlen_reference)
+from oracle.attention import (attention_grads, attention_reference, bwd_delta, causal_mask,
+                              flash_backward_tiled, flash_forward_tiled, naive_attention, varlen_reference)
 from oracle.inputs import CONFIGS, make_config_inputs, make_varlen_inputs, varlen_fwd_flops
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "attention_golden.npz")
@@ -206,6 +207,23 @@ def _broken_top_left_mask(q, k, v, causal=False, sm_scale=None):
         s = s.masked_fill(torch.ones(nq, nk, dtype=torch.bool).triu(1), float("-inf"))
     lse = torch.logsumexp(s, -1)
     return torch.exp(s - lse.unsqueeze(-1)) @ v64, lse
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_delta_identity(causal):
+    """delta_i = rowsum(dO_i * O_i) equals sum_j P_ij dP_ij with dP = dO V^T,
+    because O = P V; the right-hand side never forms O."""
+    g = torch.Generator().manual_seed(11)
+    q, k, v, do = (torch.randn(2, 3, 19, 16, generator=g, dtype=torch.float64) for _ in range(4))
+    o, _ = attention_reference(q, k, v, causal)
+    s = (q @ k.transpose(-1, -2)) / math.sqrt(16)
+    if causal:
+        s = s.masked_fill(~causal_mask(19, 19), float("-inf"))
+    p = torch.softmax(s, -1)
+    dp = do @ v.transpose(-1, -2)
+    torch.testing.assert_close(bwd_delta(o, do), (p * dp).sum(-1), atol=1e-12, rtol=1e-12)
+    # a mistake that drops the dO factor is caught
+    assert not torch.allclose(o.sum(-1), (p * dp).sum(-1))
 
 
 @pytest.mark.parametrize("broken", [_broken_scale_twice, _broken_transposed_v, _broken_top_left_mask])
