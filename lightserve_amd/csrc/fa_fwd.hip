@@ -136,15 +136,55 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   // (kept only for the logsumexp output, as the reference's l_i).
   float m_run = -1e30f, l_run = 0.f, l_lse = 0.f;
 
-  // Exponentials, rounding to the input dtype, row sum and O^T += V^T P^T.
-  // The row sum adds the rounded p that the MFMA multiplies (v_dot2 with
-  // ones), so numerator and denominator share the rounding of the dominant
-  // terms whatever the exponent offset.
-  auto body = [&](const LDS_AS char* Vs, f32x16 (&s)[KB]) {
+  // K tile t lives in buffer t&1 (smem + (t&1)*TILE), V tile t in 2 + (t&1).
+  auto kbuf = [&](int t) { return sbytes + (t & 1) * TILE * 2; };
+  auto vbuf = [&](int t) { return sbytes + (2 + (t & 1)) * TILE * 2; };
+
+  // S^T = K Q^T for one tile (fp32, unscaled).
+  auto scores = [&](const LDS_AS char* Ks, f32x16* s) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) s[kb] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const X8 a = *(const LDS_AS X8*)(Ks + kb * 32 * DP * 2 + koff[kk]);
+        s[kb] = mfma32(a, qreg[kk], s[kb]);
+      }
+    }
+  };
+  // Row max of a tile in log2 units (both lane halves hold the row's keys).
+  auto row_max = [&](const f32x16* s) -> float {
+    float mx = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+    mx = half_max(mx);
+    return mx == -INFINITY ? -INFINITY : mx * sl2;
+  };
+  // Raise the running offset only where a row max moved by more than the
+  // threshold (wave-uniform branch, taken on few tiles): O and l rescale in
+  // place.
+  auto raise_offset = [&](float mxs) {
+    if (__builtin_amdgcn_ballot_w64(mxs > m_run + kRescaleThreshold) != 0) {
+      const float m_new = fmaxf(m_run, mxs);
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
+      if constexpr (LSE) l_lse *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+    }
+  };
+  // Exponentials, rounding to the input dtype and row sums. The row sum adds
+  // the rounded p that the MFMA multiplies (v_dot2 with ones), so numerator
+  // and denominator share the rounding of the dominant terms whatever the
+  // exponent offset.
+  auto softmax = [&](f32x16* s, X8* pb) {
     const float neg_m = -m_run;
     float rs[4] = {0.f, 0.f, 0.f, 0.f};
     float re = 0.f;
-    X8 pb[2 * KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
@@ -159,6 +199,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
     }
     l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
     if constexpr (LSE) l_lse += re;
+  };
+  // O^T += V^T P^T with V^T from transpose reads.
+  auto pv = [&](const LDS_AS char* Vs, const X8* pb) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -171,34 +214,61 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
     }
   };
 
-  if (ntiles > 0) {
-    tile_load(K, p.skn, kvo, 0, 0);
-    tile_load(V, p.svn, vvo, 0, 2);
-  }
+  // Tiles [0, n_full) are fully visible to every row of the workgroup (inside
+  // the sequence and, when causal, at or below the diagonal of its first row).
+  // They run software-pipelined: while the MFMAs of S for tile j+1 issue, the
+  // VALU computes tile j's exponentials; while tile j's PV MFMAs issue, it
+  // computes tile j+1's row max. Tiles [n_full, ntiles) then run one at a
+  // time with masking. Buffers: K tile t+2 and V tile t+1 load while tile t
+  // is processed (K runs one tile ahead of V).
+  int n_full = min(ntiles, nk / BN);
+  if (CAUSAL) n_full = min(n_full, max(0, q0 + off + 1) / BN);
+
+  tile_load(K, p.skn, kvo, 0, 0);
+  tile_load(V, p.svn, vvo, 0, 2);
+  tile_load(K, p.skn, kvo, 1, 1);  // past the end the descriptor is empty: zeros
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  for (int j = 0; j < ntiles; ++j) {
-    if (j + 1 < ntiles) {
-      tile_load(K, p.skn, kvo, j + 1, (j + 1) & 1);
-      tile_load(V, p.svn, vvo, j + 1, 2 + ((j + 1) & 1));
-    }
+  f32x16 s0[KB], s1[KB];
+  if (n_full > 0) {
+    scores(kbuf(0), s0);
+    m_run = row_max(s0);  // every row sees the whole tile: finite
+    __syncthreads();      // K buffer 0 is refilled by the first step
+  }
+  // One pipelined step: tile t's scores are in cur (offset already raised),
+  // tile t+1's go to nxt.
+  auto pipe_step = [&](int t, f32x16* cur, f32x16* nxt) {
+    tile_load(K, p.skn, kvo, t + 2, t & 1);
+    tile_load(V, p.svn, vvo, t + 1, 2 + ((t + 1) & 1));
+    scores(kbuf(t + 1), nxt);
+    X8 pb[2 * KB];
+    softmax(cur, pb);
+    pv(vbuf(t), pb);
+    const float mxs = row_max(nxt);
+    if (t + 1 < n_full) raise_offset(mxs);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  };
+  int j = 0;
+  for (; j + 1 < n_full; j += 2) {
+    pipe_step(j, s0, s1);
+    pipe_step(j + 1, s1, s0);
+  }
+  if (j < n_full) {
+    pipe_step(j, s0, s1);
+    ++j;
+  }
+
+  // Remaining tiles (diagonal / sequence end), masked, one at a time. K of
+  // tile n_full + 1 is already in flight from the pipelined part.
+  for (; j < ntiles; ++j) {
+    if (j > n_full) tile_load(K, p.skn, kvo, j + 1, (j + 1) & 1);
+    tile_load(V, p.svn, vvo, j + 1, 2 + ((j + 1) & 1));
     const int kbase = j * BN;
     const bool active = !CAUSAL || (kbase <= qw_lo + 31 + off);
     if (active) {
-      const LDS_AS char* Ks = sbytes + (j & 1) * TILE * 2;
-      const LDS_AS char* Vs = sbytes + (2 + (j & 1)) * TILE * 2;
-      f32x16 s[KB];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) s[kb] = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) {
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          const X8 a = *(const LDS_AS X8*)(Ks + kb * 32 * DP * 2 + koff[kk]);
-          s[kb] = mfma32(a, qreg[kk], s[kb]);
-        }
-      }
+      scores(kbuf(j), s0);
       const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > qw_lo + off);
       if (need_mask) {
         int lim = nk - 1 - kbase - 4 * hh;
@@ -207,28 +277,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i)
-            if (32 * kb + 8 * (i >> 2) + (i & 3) > lim) s[kb][i] = -INFINITY;
+            if (32 * kb + 8 * (i >> 2) + (i & 3) > lim) s0[kb][i] = -INFINITY;
       }
-      float mx = s[0][0];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-      mx = half_max(mx);
-      const float mxs = mx == -INFINITY ? -INFINITY : mx * sl2;
-      // Raise the running offset only where a row max moved by more than the
-      // threshold (wave-uniform branch, taken on few tiles): O and l rescale
-      // in place.
-      if (__builtin_amdgcn_ballot_w64(mxs > m_run + kRescaleThreshold) != 0) {
-        const float m_new = fmaxf(m_run, mxs);
-        const float alpha = fast_exp2(m_run - m_new);
-        l_run *= alpha;
-        if constexpr (LSE) l_lse *= alpha;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-      }
-      body(Vs, s);
+      raise_offset(row_max(s0));
+      X8 pb[2 * KB];
+      softmax(s0, pb);
+      pv(vbuf(j), pb);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
