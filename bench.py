@@ -47,7 +47,8 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=2, help="heads in the CPU-baseline sample")
+    ap.add_argument("--cpu-heads", type=int, default=128,
+                    help="(batch, head) slices in the CPU-baseline sample (bounded by memory; ~10 s of CPU work)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before the warm-up, run 3 plain device copies of MIB MiB each (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters to bytes)")
@@ -93,11 +94,18 @@ def check_parity(cfg, inp, outs):
 
 def cpu_baseline(cfg, inp, n_heads, flops_full, step_kind):
     """Times F.scaled_dot_product_attention (fp32, CPU) on n_heads heads of the
-    workload (1 warm-up, median of 3) and scales to the full job."""
+    workload (1 warm-up, median of 5) and scales to the full job."""
     import torch
     import torch.nn.functional as F
-    q, k, v = (inp[n][:1, :n_heads].float().cpu() for n in ("q", "k", "v"))
-    do = inp["do"][:1, :n_heads].float().cpu() if "do" in inp else None
+    B, H, N = inp["q"].shape[:3]
+    # at most ~8 GB of fp32 score matrices (autograd keeps a few of them)
+    n_heads = max(1, min(n_heads, B * H, int(8e9 // (N * N * 4))))
+
+    def sample(t):  # the first n_heads (batch, head) slices, as [1, n_heads, N, D]
+        return t.reshape(1, B * H, *t.shape[2:])[:, :n_heads].float().cpu()
+
+    q, k, v = (sample(inp[n]) for n in ("q", "k", "v"))
+    do = sample(inp["do"]) if "do" in inp else None
     causal = inp["causal"]
 
     def run():
@@ -109,7 +117,7 @@ def cpu_baseline(cfg, inp, n_heads, flops_full, step_kind):
 
     run()
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
@@ -128,7 +136,7 @@ def cpu_baseline(cfg, inp, n_heads, flops_full, step_kind):
         "value": round(flops_full / full_s / 1e12, 4), "unit": "TFLOP/s",
         "cores": torch.get_num_threads(), "kind": "port",
         "sample": (f"F.scaled_dot_product_attention fp32 {step_kind} on {n_heads} of {total_heads} (b,h) heads "
-                   f"(1 warm-up, median of 3: {t:.2f} s), scaled linearly; os.cpu_count()={os.cpu_count()}; "
+                   f"(1 warm-up, median of 5: {t:.2f} s), scaled linearly; os.cpu_count()={os.cpu_count()}; "
                    f"{cpu_model}"),
     }
 

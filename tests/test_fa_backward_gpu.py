@@ -107,3 +107,64 @@ def test_config_backward_full_size(gpu, cfg):
                                        block_n=256, op_dtype=q.dtype)
         for name, got, ex, ra in zip(("dq", "dk", "dv"), (dq[sl], dk[sl], dv[sl]), exact, ref_alg):
             assert_grad_parity(got, ex, ra, f"config {cfg} (b={b},h={h}) {name}")
+
+
+def _abi_fwd_bwd(q, k, v, do, causal, scale):
+    """Forward with L, then backward, through the C ABI directly (the Python
+    mirror keeps the reference's square-only contract)."""
+    from lightserve_amd import _lib
+    B, H, Nq, D = q.shape
+    Nk = k.shape[2]
+    o = torch.empty_like(q)
+    L = torch.empty(B, H, Nq, device=q.device, dtype=torch.float32)
+    dt = _lib.TORCH_TO_LSFA[q.dtype]
+    fa = _lib.FwdArgs(q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), o=o.data_ptr(), lse=L.data_ptr(),
+                      q_stride=_lib.strides4(q), k_stride=_lib.strides4(k), v_stride=_lib.strides4(v),
+                      o_stride=_lib.strides4(o), lse_stride=_lib._i64x3(*L.stride()),
+                      cu_seqlens_q=None, cu_seqlens_k=None, dtype=dt, batch=B, heads_q=H, heads_kv=H,
+                      seqlen_q=Nq, seqlen_k=Nk, head_dim=D, causal=int(causal), sm_scale=scale, reserved=0)
+    stream = _lib.current_stream(q.device)
+    _lib.fwd(fa, stream)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ba = _lib.BwdArgs(q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), o=o.data_ptr(), dout=do.data_ptr(),
+                      lse=L.data_ptr(), dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(), workspace=None,
+                      workspace_bytes=0, q_stride=_lib.strides4(q), k_stride=_lib.strides4(k),
+                      v_stride=_lib.strides4(v), o_stride=_lib.strides4(o), do_stride=_lib.strides4(do),
+                      dq_stride=_lib.strides4(dq), dk_stride=_lib.strides4(dk), dv_stride=_lib.strides4(dv),
+                      lse_stride=_lib._i64x3(*L.stride()), cu_seqlens_q=None, cu_seqlens_k=None, dtype=dt,
+                      batch=B, heads_q=H, heads_kv=H, seqlen_q=Nq, seqlen_k=Nk, head_dim=D,
+                      causal=int(causal), sm_scale=scale, reserved=0)
+    n = _lib.bwd_workspace_size(ba)
+    ws = torch.empty(max(n, 1), device=q.device, dtype=torch.uint8)
+    ba.workspace, ba.workspace_bytes = ws.data_ptr(), n
+    _lib.bwd(ba, stream)
+    return o, L, dq, dk, dv
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Nq,Nk", [(70, 200), (200, 70), (1, 129), (129, 1)])
+def test_abi_backward_non_square(gpu, Nq, Nk, causal, dtype):
+    """Nq != Nk through the C ABI: causal masking is bottom-right aligned
+    (query i sees keys <= i + Nk - Nq); rows that see no key get zero
+    gradients and L = -inf."""
+    print(f"case abi bwd Nq={Nq} Nk={Nk} causal={causal} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    B, H, D = 2, 3, 64
+    q, do = (torch.randn(B, H, Nq, D, generator=g).to(dtype).to(gpu) for _ in range(2))
+    k, v = (torch.randn(B, H, Nk, D, generator=g).to(dtype).to(gpu) for _ in range(2))
+    scale = D ** -0.5
+    o, L, dq, dk, dv = _abi_fwd_bwd(q, k, v, do, causal, scale)
+    torch.cuda.synchronize()
+    qc, kc, vc, doc = (t.cpu() for t in (q, k, v, do))
+    o_ref, l_ref = attention_reference(qc, kc, vc, causal, scale)
+    refs = attention_grads(qc, kc, vc, doc, causal, scale)
+    seen = torch.isfinite(l_ref)
+    assert torch.equal(torch.isfinite(L.cpu()), seen)
+    tol = 1e-4 if dtype == torch.float32 else 3e-2
+    torch.testing.assert_close(L.cpu()[seen].double(), l_ref[seen], atol=1e-3 if dtype != torch.float32 else 1e-5,
+                               rtol=0)
+    torch.testing.assert_close(o.cpu().double().nan_to_num(), o_ref.nan_to_num(), atol=tol, rtol=tol)
+    for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), refs):
+        torch.testing.assert_close(got.cpu().double(), ref.nan_to_num(), atol=tol, rtol=tol,
+                                   msg=lambda m: f"{name}: {m}")
