@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define LSFA_ABI_VERSION 2
+#define LSFA_ABI_VERSION 3
 
 typedef enum {
   LSFA_DTYPE_FP32 = 0,
@@ -129,6 +129,54 @@ typedef struct {
   int32_t reserved;
 } lsfa_bwd_args;
 
+/* Paged-KV decode arguments: one new query token per sequence against a KV
+ * cache addressed through block tables. The reference has no such kernel;
+ * its engine documents it as the missing decode path (engine/README.md,
+ * "No decode-shaped attention kernel": Nq = 1 against a paged Nkv, gathering
+ * K/V across a request's block_table).
+ *   q          [batch, heads_q, head_dim]
+ *   k_cache,
+ *   v_cache    [num_blocks, block_size, heads_kv, head_dim] (a block holds
+ *              block_size x n_kv_heads x head_dim elements per layer,
+ *              engine/config.py:5-7)
+ *   block_tables int32 [batch, max_blocks_per_seq]; entry i holds the
+ *              physical block of tokens [i*block_size, (i+1)*block_size)
+ *              (engine/block_manager.py:56-60)
+ *   seq_lens   int32 [batch]: cached tokens per sequence, the new token's K/V
+ *              included; clamped on the device to max_seq_len and to
+ *              max_blocks_per_seq * block_size
+ *   o          like q; lse fp32 [batch, heads_q] (natural log) or NULL
+ * Query head h reads KV head h / (heads_q / heads_kv). Block ids outside
+ * [0, num_blocks) read as zeros. workspace: lsfa_decode_workspace_size()
+ * bytes, 256-byte aligned (0 bytes when no sequence is split). */
+typedef struct {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  void* o;
+  float* lse;
+  const int32_t* block_tables;
+  const int32_t* seq_lens;
+  void* workspace;
+  uint64_t workspace_bytes;
+  int64_t q_stride[3];         /* batch, head, dim */
+  int64_t k_stride[4];         /* block, slot, head, dim */
+  int64_t v_stride[4];
+  int64_t o_stride[3];
+  int64_t lse_stride[2];
+  int64_t block_table_stride;  /* elements between consecutive sequences' tables */
+  int32_t dtype;               /* bf16 or fp16 */
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;            /* heads_q / heads_kv in {1, 2, 4, 8} */
+  int32_t head_dim;            /* multiple of 8, at most 128 */
+  int32_t block_size;          /* power of two */
+  int32_t num_blocks;
+  int32_t max_blocks_per_seq;
+  int32_t max_seq_len;         /* upper bound of seq_lens (sets the split) */
+  float sm_scale;
+} lsfa_decode_args;
+
 /* ABI version of the loaded library (LSFA_ABI_VERSION). */
 int lsfa_abi_version(void);
 
@@ -157,6 +205,17 @@ int lsfa_bwd_workspace_size(const lsfa_bwd_args* args, uint64_t* bytes);
  * (kernels/flash_attention_backward.py:341-350), the backward launch
  * (:363-381) and the fp32->dtype cast of dq (:382). */
 int lsfa_bwd(const lsfa_bwd_args* args, void* stream);
+
+/* Host-only validation of decode arguments; never touches the GPU. */
+int lsfa_decode_check(const lsfa_decode_args* args);
+
+/* Workspace bytes lsfa_decode needs (split partial outputs); no GPU work. */
+int lsfa_decode_workspace_size(const lsfa_decode_args* args, uint64_t* bytes);
+
+/* Paged-KV decode: o = softmax(q K^T * sm_scale) V over each sequence's
+ * seq_lens[b] cached tokens (and lse if requested). No reference
+ * counterpart (see lsfa_decode_args). */
+int lsfa_decode(const lsfa_decode_args* args, void* stream);
 
 #ifdef __cplusplus
 }

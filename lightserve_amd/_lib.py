@@ -13,7 +13,7 @@ import torch
 
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
 TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}
@@ -21,7 +21,8 @@ TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfl
 STATUS = {0: "LSFA_OK", -1: "LSFA_ERR_INVALID", -2: "LSFA_ERR_UNSUPPORTED", -3: "LSFA_ERR_LAUNCH"}
 
 EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "lsfa_fwd",
-                    "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd")
+                    "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd",
+                    "lsfa_decode_check", "lsfa_decode_workspace_size", "lsfa_decode")
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -60,6 +61,25 @@ class BwdArgs(ctypes.Structure):
     ]
 
 
+_i64x2 = ctypes.c_int64 * 2
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of lsfa_decode_args."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("block_tables", ctypes.c_void_p), ("seq_lens", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64),
+        ("q_stride", _i64x3), ("k_stride", _i64x4), ("v_stride", _i64x4), ("o_stride", _i64x3),
+        ("lse_stride", _i64x2), ("block_table_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("block_size", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32), ("max_blocks_per_seq", ctypes.c_int32),
+        ("max_seq_len", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -85,16 +105,19 @@ def load():
         lib.lsfa_abi_version.argtypes = []
         lib.lsfa_last_error.restype = ctypes.c_char_p
         lib.lsfa_last_error.argtypes = []
-        for name, struct in (("lsfa_fwd_check", FwdArgs), ("lsfa_bwd_check", BwdArgs)):
+        for name, struct in (("lsfa_fwd_check", FwdArgs), ("lsfa_bwd_check", BwdArgs),
+                             ("lsfa_decode_check", DecodeArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct)]
-        for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs)):
+        for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_decode", DecodeArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
         lib.lsfa_bwd_workspace_size.restype = ctypes.c_int
         lib.lsfa_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdArgs), ctypes.POINTER(ctypes.c_uint64)]
+        lib.lsfa_decode_workspace_size.restype = ctypes.c_int
+        lib.lsfa_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_uint64)]
         version = lib.lsfa_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"{_LIB_NAME} has ABI version {version}, expected {ABI_VERSION}")
@@ -126,6 +149,23 @@ def bwd_workspace_size(args):
     n = ctypes.c_uint64(0)
     _raise_on(load().lsfa_bwd_workspace_size(ctypes.byref(args), ctypes.byref(n)), "lsfa_bwd_workspace_size")
     return n.value
+
+
+def decode_check(args):
+    lib = load()
+    rc = lib.lsfa_decode_check(ctypes.byref(args))
+    return rc, lib.lsfa_last_error().decode(errors="replace")
+
+
+def decode_workspace_size(args):
+    """Bytes of device workspace lsfa_decode needs (host only; 0 when unsplit)."""
+    n = ctypes.c_uint64(0)
+    _raise_on(load().lsfa_decode_workspace_size(ctypes.byref(args), ctypes.byref(n)), "lsfa_decode_workspace_size")
+    return n.value
+
+
+def decode(args, stream):
+    _raise_on(load().lsfa_decode(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_decode")
 
 
 def fwd(args, stream):

@@ -1,5 +1,6 @@
 // C ABI of liblsfa_gfx950.so: argument validation (host only, no GPU access)
 // and kernel selection. See include/lightserve_fa.h for the contract.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -14,6 +15,7 @@ hipError_t fwd_mfma(FwdParams p, bool is_bf16, int dp, bool causal, bool varlen,
 hipError_t bwd_mfma(const BwdParams& p, bool is_bf16, int dp, bool causal, hipStream_t s);
 hipError_t fwd_f32(const FwdParams& p, int dp, bool causal, bool varlen, float scale, hipStream_t s);
 hipError_t bwd_f32(const BwdParams& p, int dp, bool causal, hipStream_t s);
+hipError_t decode_gqa(const DecodeParams& p, bool is_bf16, int dp, hipStream_t s);
 }  // namespace lsfa
 
 namespace {
@@ -38,6 +40,7 @@ int ok() {
 
 // Padded head dim of the kernels: 32, 64 or 128.
 int padded_dim(int d) { return d <= 32 ? 32 : (d <= 64 ? 64 : 128); }
+int padded_decode_dim(int d) { return d <= 64 ? 64 : 128; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -94,6 +97,43 @@ BwdWorkspace bwd_workspace(int dtype, int batch, int heads, int nq, int head_dim
     w.bytes += 2 * tb;
   }
   return w;
+}
+
+// Decode split: enough workgroups (batch x kv heads x splits) to fill the
+// GPU, splits of a multiple of 64 tokens whose block-table slice fits the
+// kernel's LDS table. Partial outputs go to the workspace when split.
+struct DecodeSplit {
+  int num_splits = 1, split_tokens = 64;
+  uint64_t o_off = 0, lse_off = 0, bytes = 0;
+};
+
+int log2_exact(int x) {
+  int s = 0;
+  while ((1 << s) < x) ++s;
+  return (1 << s) == x ? s : -1;
+}
+
+DecodeSplit decode_split(const lsfa_decode_args* a) {
+  DecodeSplit d;
+  const int maxs = std::max(a->max_seq_len, 0);
+  const long long units = std::max(1LL, (long long)a->batch * a->heads_kv);
+  long long ns = 1;
+  if (units < 1024 && maxs > 256) ns = std::min<long long>((1024 + units - 1) / units, (maxs + 255) / 256);
+  long long st = (maxs + ns - 1) / ns;
+  st = std::max(64LL, (st + 63) / 64 * 64);
+  const int shift = std::max(0, log2_exact(std::max(1, a->block_size)));
+  const long long max_st = ((long long)(lsfa::kDecodeMaxTableSlots - 1) << shift) / 64 * 64;
+  st = std::min(st, std::max(64LL, max_st));
+  ns = std::max(1LL, (maxs + st - 1) / st);
+  d.num_splits = (int)ns;
+  d.split_tokens = (int)st;
+  if (ns > 1) {
+    const uint64_t rows = (uint64_t)a->batch * a->heads_q * ns;
+    d.o_off = 0;
+    d.lse_off = align256(rows * padded_decode_dim(a->head_dim) * 4);
+    d.bytes = d.lse_off + align256(rows * 4);
+  }
+  return d;
 }
 
 }  // namespace
@@ -242,6 +282,93 @@ int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
   else
     e = lsfa::bwd_mfma(p, a->dtype == LSFA_DTYPE_BF16, dp, a->causal != 0, s);
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int lsfa_decode_check(const lsfa_decode_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  if (a->dtype != LSFA_DTYPE_FP16 && a->dtype != LSFA_DTYPE_BF16)
+    return fail(a->dtype == LSFA_DTYPE_FP32 ? LSFA_ERR_UNSUPPORTED : LSFA_ERR_INVALID,
+                "decode supports bf16 and fp16 (dtype %d)", a->dtype);
+  if (a->batch < 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->num_blocks < 0 || a->max_blocks_per_seq < 0 ||
+      a->max_seq_len < 0)
+    return fail(LSFA_ERR_INVALID, "negative size or no heads (batch=%d heads_q=%d heads_kv=%d num_blocks=%d "
+                "max_blocks_per_seq=%d max_seq_len=%d)", a->batch, a->heads_q, a->heads_kv, a->num_blocks,
+                a->max_blocks_per_seq, a->max_seq_len);
+  if (a->heads_q % a->heads_kv != 0) return fail(LSFA_ERR_INVALID, "heads_q (%d) is not a multiple of heads_kv (%d)", a->heads_q, a->heads_kv);
+  const int g = a->heads_q / a->heads_kv;
+  if (g != 1 && g != 2 && g != 4 && g != 8)
+    return fail(LSFA_ERR_UNSUPPORTED, "heads_q / heads_kv = %d; decode supports 1, 2, 4 and 8", g);
+  if (a->head_dim < 8 || a->head_dim > 128 || a->head_dim % 8 != 0)
+    return fail(LSFA_ERR_UNSUPPORTED, "decode head_dim must be a multiple of 8 in 8..128 (got %d)", a->head_dim);
+  if (a->block_size < 1 || log2_exact(a->block_size) < 0)
+    return fail(LSFA_ERR_UNSUPPORTED, "block_size must be a power of two (got %d)", a->block_size);
+  if (!std::isfinite(a->sm_scale)) return fail(LSFA_ERR_INVALID, "sm_scale is not finite");
+  if (a->batch == 0) return ok();
+  if (!a->q || !a->k_cache || !a->v_cache || !a->o || !a->block_tables || !a->seq_lens)
+    return fail(LSFA_ERR_INVALID, "q, k_cache, v_cache, o, block_tables and seq_lens must be non-NULL");
+  if (a->q_stride[2] != 1 || a->o_stride[2] != 1 || a->k_stride[3] != 1 || a->v_stride[3] != 1)
+    return fail(LSFA_ERR_UNSUPPORTED, "head-dim strides must be 1");
+  for (int i = 0; i < 2; ++i)
+    if (a->q_stride[i] % 8 != 0 || a->o_stride[i] % 8 != 0)
+      return fail(LSFA_ERR_UNSUPPORTED, "q/o strides must be multiples of 8 elements");
+  for (int i = 0; i < 3; ++i)
+    if (a->k_stride[i] % 8 != 0 || a->v_stride[i] % 8 != 0)
+      return fail(LSFA_ERR_UNSUPPORTED, "k_cache/v_cache strides must be multiples of 8 elements");
+  if (!aligned16(a->q) || !aligned16(a->o) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+    return fail(LSFA_ERR_UNSUPPORTED, "q, o, k_cache and v_cache must be 16-byte aligned");
+  if (a->block_table_stride < a->max_blocks_per_seq)
+    return fail(LSFA_ERR_INVALID, "block_table_stride %lld is below max_blocks_per_seq %d",
+                (long long)a->block_table_stride, a->max_blocks_per_seq);
+  const DecodeSplit d = decode_split(a);
+  if (d.bytes > 0) {
+    if (!a->workspace) return fail(LSFA_ERR_INVALID, "workspace must be non-NULL");
+    if (a->workspace_bytes < d.bytes)
+      return fail(LSFA_ERR_INVALID, "workspace_bytes %llu is below the %llu bytes lsfa_decode_workspace_size asks for",
+                  (unsigned long long)a->workspace_bytes, (unsigned long long)d.bytes);
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
+      return fail(LSFA_ERR_INVALID, "workspace is not 256-byte aligned");
+  }
+  return ok();
+}
+
+int lsfa_decode_workspace_size(const lsfa_decode_args* a, uint64_t* bytes) {
+  if (a == nullptr || bytes == nullptr) return fail(LSFA_ERR_INVALID, "args or bytes is NULL");
+  *bytes = decode_split(a).bytes;
+  return ok();
+}
+
+int lsfa_decode(const lsfa_decode_args* a, void* stream) {
+  int rc = lsfa_decode_check(a);
+  if (rc) return rc;
+  if (a->batch == 0) return ok();
+  const DecodeSplit d = decode_split(a);
+  lsfa::DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = a->q; p.kc = a->k_cache; p.vc = a->v_cache; p.o = a->o; p.lse = a->lse;
+  p.block_tables = a->block_tables; p.seq_lens = a->seq_lens;
+  if (d.bytes > 0) {
+    char* ws = static_cast<char*>(a->workspace);
+    p.o_part = reinterpret_cast<float*>(ws + d.o_off);
+    p.lse_part = reinterpret_cast<float*>(ws + d.lse_off);
+  }
+  p.sqb = a->q_stride[0]; p.sqh = a->q_stride[1];
+  p.skb = a->k_stride[0]; p.sks = a->k_stride[1]; p.skh = a->k_stride[2];
+  p.svb = a->v_stride[0]; p.svs = a->v_stride[1]; p.svh = a->v_stride[2];
+  p.sob = a->o_stride[0]; p.soh = a->o_stride[1];
+  p.slb = a->lse_stride[0]; p.slh = a->lse_stride[1];
+  p.sbt = a->block_table_stride;
+  p.B = a->batch; p.Hq = a->heads_q; p.Hkv = a->heads_kv; p.D = a->head_dim;
+  p.block_shift = log2_exact(a->block_size);
+  p.max_blocks = a->max_blocks_per_seq;
+  p.num_blocks = a->num_blocks;
+  p.max_seq_len = a->max_seq_len;
+  p.num_splits = d.num_splits;
+  p.split_tokens = d.split_tokens;
+  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  hipError_t e = lsfa::decode_gqa(p, a->dtype == LSFA_DTYPE_BF16, padded_decode_dim(a->head_dim),
+                                  reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

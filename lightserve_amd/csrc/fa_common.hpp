@@ -175,6 +175,33 @@ struct BwdParams {
   float scale_log2;  // sm_scale * log2(e)
 };
 
+// Paged-KV decode (one query token per sequence); strides in elements.
+constexpr int kDecodeMaxTableSlots = 512;  // block-table entries one split may span
+struct DecodeParams {
+  const void* q;       // [B, Hq, D]
+  const void* kc;      // [num_blocks, block_size, Hkv, D]
+  const void* vc;
+  void* o;             // [B, Hq, D]
+  float* lse;          // [B, Hq] or null
+  const int32_t* block_tables;  // [B, max_blocks]
+  const int32_t* seq_lens;      // [B]
+  float* o_part;       // [B, Hq, num_splits, DP] (split path)
+  float* lse_part;     // [B, Hq, num_splits]
+  int64_t sqb, sqh;
+  int64_t skb, sks, skh;  // k cache: block, slot, head strides
+  int64_t svb, svs, svh;
+  int64_t sob, soh;
+  int64_t slb, slh;
+  int64_t sbt;            // block table row stride
+  int B, Hq, Hkv, D;
+  int block_shift;        // log2(block_size)
+  int max_blocks;         // block-table entries per sequence
+  int num_blocks;         // blocks in the cache; other ids read as zero
+  int max_seq_len;        // sequences are clamped to min(this, max_blocks * block_size)
+  int num_splits, split_tokens;  // split_tokens is a multiple of 16
+  float scale_log2;       // sm_scale * log2(e)
+};
+
 // Maps the 1-D launch index to (batch*head, tile). Workgroups are handed to
 // the 8 XCDs round-robin by launch index, so consecutive launch indices are
 // spread so that each XCD owns a contiguous run of heads (their K/V stay in

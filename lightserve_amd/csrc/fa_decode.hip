@@ -1,0 +1,258 @@
+// Paged-KV decode attention for gfx950 (one new query token per sequence).
+//
+// The reference's engine keeps per-request block tables of physical KV-cache
+// block ids (engine/block_manager.py:56-60: table entry i holds tokens
+// [i*block_size, (i+1)*block_size)) and documents the missing kernel: decode
+// needs Nq = 1 against a paged Nkv, gathering K/V across the block table
+// (engine/README.md, "No decode-shaped attention kernel"; engine/request.py
+// is_prefill). A block holds block_size x n_kv_heads x head_dim elements per
+// layer for K and for V (engine/config.py:5-7); here the cache tensors are
+// [num_blocks, block_size, Hkv, D] with element strides.
+//
+// The path is HBM-bound (each K/V byte is used by Hq/Hkv query heads: about
+// 4 FLOP per byte), so the kernel is built around coalesced streaming:
+//   fa_decode_split_kernel: one workgroup per (sequence, KV head, split of
+//     the sequence). With D = 128 a wave reads 4 tokens per load
+//     instruction: lane (tq, c) = (lane / 16, lane % 16) loads 16 bytes
+//     (8 dims) of token tq, so a token's 256-byte row is one contiguous
+//     16-lane access. Each lane keeps q for its 8 dims and all G = Hq/Hkv
+//     query heads in registers, partial dot products are summed across the
+//     16 lanes with butterfly shuffles, and every lane group runs its own
+//     online softmax over its tokens (exponent offset raised per 4-token
+//     chunk). The split's block-table slice is staged in LDS first. Lane
+//     groups merge with shuffles, waves through LDS.
+//   fa_decode_combine_kernel: when a sequence is split, merges the splits'
+//     normalised partial outputs with their logsumexps.
+#include "fa_common.hpp"
+
+namespace lsfa {
+
+constexpr float kDecLn2 = 0.6931471805599453f;
+
+template <int DP>
+__device__ __forceinline__ float group_sum(float x) {
+  // sum over the DP/8 lanes that hold one token's row
+#pragma unroll
+  for (int m = DP / 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, DP / 8);
+  return x;
+}
+
+template <typename T, int DP, int G>
+__global__ __launch_bounds__(256) void fa_decode_split_kernel(const DecodeParams p) {
+  using X8 = typename VecT<T>::x8;
+  constexpr int LPT = DP / 8;    // lanes per token row (16 B each)
+  constexpr int TPW = 64 / LPT;  // tokens per wave per load instruction
+  constexpr int NW = 4;
+  constexpr int TPI = NW * TPW;  // tokens per workgroup per load instruction
+  constexpr int CH = 4;          // tokens per lane group between offset updates
+
+  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane % LPT, tq = lane / LPT;
+  const int seq = min(max(p.seq_lens[b], 0), min(p.max_seq_len, p.max_blocks << p.block_shift));
+  const int t0 = split * p.split_tokens;
+  const int t1 = min(seq, t0 + p.split_tokens);
+
+  __shared__ int s_blk[kDecodeMaxTableSlots];
+  __shared__ float st_m[NW][G], st_l[NW][G];
+  __shared__ float st_o[NW][G][DP];
+
+  // The split's slice of the block table (the host keeps it within
+  // kDecodeMaxTableSlots entries).
+  const int first_slot = t0 >> p.block_shift;
+  const int n_slots = t1 > t0 ? ((t1 - 1) >> p.block_shift) - first_slot + 1 : 0;
+  const int32_t* table = p.block_tables + (int64_t)b * p.sbt + first_slot;
+  for (int i = tid; i < n_slots; i += 256) s_blk[i] = table[i];
+
+  // q of the G query heads of this KV head, dims 8c..8c+7, pre-scaled to
+  // log2 units.
+  float qf[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int h = hk * G + g;
+    u32x4 raw = {0, 0, 0, 0};
+    if (8 * c < p.D) raw = ldg16((const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh + 8 * c);
+    const X8 v = __builtin_bit_cast(X8, raw);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[g][e] = (float)v[e] * p.scale_log2;
+  }
+  __syncthreads();
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
+
+  const T* kbase = (const T*)p.kc + (int64_t)hk * p.skh + 8 * c;
+  const T* vbase = (const T*)p.vc + (int64_t)hk * p.svh + 8 * c;
+  const bool col_ok = 8 * c < p.D;
+  const int bmask = (1 << p.block_shift) - 1;
+
+  // Every lane group (wave, tq) walks its own tokens: scores of a chunk of
+  // CH tokens, one offset update, then the weighted V sum.
+  for (int tb = t0 + wave * TPW + tq; tb < t1; tb += CH * TPI) {
+    float s[CH][G];
+    X8 vv[CH];
+    bool ok[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int t = tb + u * TPI;
+      ok[u] = t < t1;
+      u32x4 kr = {0, 0, 0, 0}, vr = {0, 0, 0, 0};
+      const int blk = ok[u] ? s_blk[(t >> p.block_shift) - first_slot] : 0;
+      if (ok[u] && col_ok && (unsigned)blk < (unsigned)p.num_blocks) {
+        const int slot = t & bmask;
+        kr = ldg16(kbase + (int64_t)blk * p.skb + (int64_t)slot * p.sks);
+        vr = ldg16(vbase + (int64_t)blk * p.svb + (int64_t)slot * p.svs);
+      }
+      const X8 kv = __builtin_bit_cast(X8, kr);
+      vv[u] = __builtin_bit_cast(X8, vr);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qf[g][e], (float)kv[e], d);
+        s[u][g] = d;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+#pragma unroll
+      for (int g = 0; g < G; ++g) s[u][g] = ok[u] ? group_sum<DP>(s[u][g]) : -INFINITY;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = m[g];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) mx = fmaxf(mx, s[u][g]);
+      if (mx > m[g]) {  // uniform within the lane group
+        const float alpha = fast_exp2(m[g] - mx);
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
+        m[g] = mx;
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const float pv = ok[u] ? fast_exp2(s[u][g] - m[g]) : 0.f;
+        l[g] += pv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv, (float)vv[u][e], acc[g][e]);
+      }
+    }
+  }
+
+  // Merge the wave's TPW lane groups (lanes with equal c) with shuffles, then
+  // the NW waves through LDS. States are (m, l, acc) in log2 units; an empty
+  // state has m = -inf and contributes weight 0.
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float M = m[g];
+#pragma unroll
+    for (int msk = LPT; msk < 64; msk <<= 1) M = fmaxf(M, __shfl_xor(M, msk));
+    const float w = M == -INFINITY ? 0.f : fast_exp2(m[g] - M);
+    float L = w * l[g];
+#pragma unroll
+    for (int msk = LPT; msk < 64; msk <<= 1) L += __shfl_xor(L, msk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float o = w * acc[g][e];
+#pragma unroll
+      for (int msk = LPT; msk < 64; msk <<= 1) o += __shfl_xor(o, msk);
+      acc[g][e] = o;
+    }
+    if (lane == 0) {
+      st_m[wave][g] = M;
+      st_l[wave][g] = L;
+    }
+    if (tq == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) st_o[wave][g][8 * c + e] = acc[g][e];
+    }
+  }
+  __syncthreads();
+
+  for (int idx = tid; idx < G * DP; idx += 256) {
+    const int g = idx / DP, d = idx % DP;
+    float M = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < NW; ++r) M = fmaxf(M, st_m[r][g]);
+    float L = 0.f, O = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int r = 0; r < NW; ++r) {
+        const float w = fast_exp2(st_m[r][g] - M);
+        L += w * st_l[r][g];
+        O += w * st_o[r][g][d];
+      }
+    }
+    const int h = hk * G + g;
+    const float on = L > 0.f ? O / L : 0.f;
+    const float lse2 = L > 0.f ? M + __log2f(L) : -INFINITY;  // log2 units
+    if (p.num_splits == 1) {
+      if (d < p.D) ((T*)p.o)[(int64_t)b * p.sob + (int64_t)h * p.soh + d] = (T)on;
+      if (d == 0 && p.lse != nullptr) p.lse[(int64_t)b * p.slb + (int64_t)h * p.slh] = lse2 * kDecLn2;
+    } else {
+      const int64_t row = ((int64_t)b * p.Hq + h) * p.num_splits + split;
+      p.o_part[row * DP + d] = on;
+      if (d == 0) p.lse_part[row] = lse2;
+    }
+  }
+}
+
+// Merges the splits of one (sequence, query head): o = sum_s w_s o_s / sum_s
+// w_s with w_s = 2^(lse_s - max lse); lse = max + log2(sum w) (log2 units in
+// the workspace, natural log in the output).
+template <typename T, int DP>
+__global__ __launch_bounds__(DP) void fa_decode_combine_kernel(const DecodeParams p) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int64_t row0 = ((int64_t)b * p.Hq + h) * p.num_splits;
+  const int seq = min(max(p.seq_lens[b], 0), min(p.max_seq_len, p.max_blocks << p.block_shift));
+  const int ns = min(p.num_splits, (seq + p.split_tokens - 1) / p.split_tokens);
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, p.lse_part[row0 + s]);
+  float W = 0.f, O = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < ns; ++s) {
+      const float w = fast_exp2(p.lse_part[row0 + s] - M);
+      W += w;
+      O += w * p.o_part[(row0 + s) * DP + d];
+    }
+  }
+  if (d < p.D) ((T*)p.o)[(int64_t)b * p.sob + (int64_t)h * p.soh + d] = (T)(W > 0.f ? O / W : 0.f);
+  if (d == 0 && p.lse != nullptr)
+    p.lse[(int64_t)b * p.slb + (int64_t)h * p.slh] = W > 0.f ? (M + __log2f(W)) * kDecLn2 : -INFINITY;
+}
+
+template <typename T, int DP, int G>
+static hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
+  hipLaunchKernelGGL((fa_decode_split_kernel<T, DP, G>), dim3(p.num_splits, p.Hkv, p.B), dim3(256), 0, s, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.num_splits == 1) return e;
+  hipLaunchKernelGGL((fa_decode_combine_kernel<T, DP>), dim3(p.Hq, p.B), dim3(DP), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T, int DP>
+static hipError_t dispatch_decode_g(const DecodeParams& p, hipStream_t s) {
+  switch (p.Hq / p.Hkv) {
+    case 1: return launch_decode<T, DP, 1>(p, s);
+    case 2: return launch_decode<T, DP, 2>(p, s);
+    case 4: return launch_decode<T, DP, 4>(p, s);
+    case 8: return launch_decode<T, DP, 8>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Host entry used by the C ABI layer (arguments already validated): dp is 64
+// or 128; the group size Hq/Hkv is 1, 2, 4 or 8.
+hipError_t decode_gqa(const DecodeParams& p, bool is_bf16, int dp, hipStream_t s) {
+  if (is_bf16) return dp == 64 ? dispatch_decode_g<__bf16, 64>(p, s) : dispatch_decode_g<__bf16, 128>(p, s);
+  return dp == 64 ? dispatch_decode_g<_Float16, 64>(p, s) : dispatch_decode_g<_Float16, 128>(p, s);
+}
+
+}  // namespace lsfa

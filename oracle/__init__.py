@@ -9,8 +9,8 @@ Contents
   attention.py  closed-form attention in float64 (the reference's test oracle,
                 kernels/tests/test_flash_attention.py:47), its autograd
                 gradients, a line-by-line restatement of the reference's
-                tiled forward/backward loops, varlen/GQA, and a pure-Python
-                loop version for tiny inputs.
+                tiled forward/backward loops, varlen/GQA, paged-KV decode,
+                and a pure-Python loop version for tiny inputs.
   inputs.py     the seeded input recipe of the five BASELINE configurations.
 
 How each function is pinned (tests/test_oracle.py):
@@ -20,6 +20,9 @@ How each function is pinned (tests/test_oracle.py):
   flash_forward_tiled   attention_reference (fp32 operands: 1e-6).
   flash_backward_tiled  attention_grads (fp32 operands: 1e-6).
   varlen_reference      pure-Python loops with GQA and bottom-right masking.
+  paged_decode_reference  pure-Python loops over a hand-built cache, the
+                        dense closed form through an identity block table,
+                        and invariance under a permutation of the blocks.
 Every function has at least one check that a planted mistake (a dropped
 scale, a transposed operand, a wrong mask offset) fails.
 """

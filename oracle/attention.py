@@ -183,3 +183,32 @@ def naive_attention(q, k, v, causal=False, sm_scale=None, group=1):
         o_all.append(o_h)
         lse_all.append(lse_h)
     return o_all, lse_all
+
+
+def paged_decode_reference(q, k_cache, v_cache, block_tables, seq_lens, sm_scale=None, *, dtype=torch.float64):
+    """Decode attention over a paged KV cache: for each sequence b, gather its
+    seq_lens[b] tokens through block_tables[b] (entry i holds tokens
+    [i*block_size, (i+1)*block_size), engine/block_manager.py:56-60), expand
+    the KV heads to the query heads (h -> h // group) and apply
+    attention_reference without a mask (the new token sees every cached
+    token). q [B, Hq, D]; caches [num_blocks, block_size, Hkv, D].
+    Returns (o [B, Hq, D], lse [B, Hq]); a sequence of length 0 gives o = 0,
+    lse = -inf."""
+    B, Hq, D = q.shape
+    bs, Hkv = k_cache.shape[1], k_cache.shape[2]
+    group = Hq // Hkv
+    outs, lses = [], []
+    for b in range(B):
+        n = int(seq_lens[b])
+        nblk = (n + bs - 1) // bs
+        ids = block_tables[b, :nblk].long().cpu()
+        k = k_cache.cpu()[ids].reshape(nblk * bs, Hkv, D)[:n].transpose(0, 1).repeat_interleave(group, 0)
+        v = v_cache.cpu()[ids].reshape(nblk * bs, Hkv, D)[:n].transpose(0, 1).repeat_interleave(group, 0)
+        if n == 0:
+            outs.append(torch.zeros(Hq, D, dtype=dtype))
+            lses.append(torch.full((Hq,), float("-inf"), dtype=dtype))
+            continue
+        o, lse = attention_reference(q[b].cpu().unsqueeze(1), k, v, False, sm_scale, dtype=dtype)
+        outs.append(o[:, 0])
+        lses.append(lse[:, 0])
+    return torch.stack(outs), torch.stack(lses)

@@ -106,8 +106,9 @@ def test_struct_layout_matches_header(built_library):
     if cc is None:
         pytest.skip("no host C compiler")
     src = ('#include <stdio.h>\n#include <stddef.h>\n#include "lightserve_fa.h"\n'
-           'int main(void){printf("%zu %zu %zu %zu\\n", sizeof(lsfa_fwd_args), sizeof(lsfa_bwd_args),'
-           ' offsetof(lsfa_fwd_args, sm_scale), offsetof(lsfa_bwd_args, sm_scale)); return 0;}\n')
+           'int main(void){printf("%zu %zu %zu %zu %zu %zu %zu\\n", sizeof(lsfa_fwd_args), sizeof(lsfa_bwd_args),'
+           ' offsetof(lsfa_fwd_args, sm_scale), offsetof(lsfa_bwd_args, sm_scale), sizeof(lsfa_decode_args),'
+           ' offsetof(lsfa_decode_args, block_table_stride), offsetof(lsfa_decode_args, sm_scale)); return 0;}\n')
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "t.c")
         exe = os.path.join(d, "t")
@@ -115,7 +116,8 @@ def test_struct_layout_matches_header(built_library):
         subprocess.run([cc, "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
         sizes = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
     assert sizes == [ctypes.sizeof(_lib.FwdArgs), ctypes.sizeof(_lib.BwdArgs),
-                     _lib.FwdArgs.sm_scale.offset, _lib.BwdArgs.sm_scale.offset]
+                     _lib.FwdArgs.sm_scale.offset, _lib.BwdArgs.sm_scale.offset, ctypes.sizeof(_lib.DecodeArgs),
+                     _lib.DecodeArgs.block_table_stride.offset, _lib.DecodeArgs.sm_scale.offset]
 
 
 def _fwd_args(**kw):

@@ -8,6 +8,8 @@ Checks, per oracle function:
   flash_backward_tiled (restated reference backward) vs attention_grads;
   bwd_delta            vs the identity delta_i = sum_j P_ij dP_ij;
   varlen_reference     vs pure-Python loops with GQA;
+  paged_decode_reference vs pure-Python loops on a cache the test scatters
+                       itself, and invariance under a block permutation;
 and planted mistakes in copies of the oracle must fail these checks.
 """
 import math
@@ -19,7 +21,8 @@ import torch
 import torch.nn.functional as F
 
 from oracle.attention import (attention_grads, attention_reference, bwd_delta, causal_mask,
-                              flash_backward_tiled, flash_forward_tiled, naive_attention, varlen_reference)
+                              flash_backward_tiled, flash_forward_tiled, naive_attention,
+                              paged_decode_reference, varlen_reference)
 from oracle.inputs import CONFIGS, make_config_inputs, make_varlen_inputs, varlen_fwd_flops
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "attention_golden.npz")
@@ -155,6 +158,58 @@ def test_varlen_matches_loops():
                                  v[ks:ke].transpose(0, 1).tolist(), True, None, group=2)
         np.testing.assert_allclose(o[qs:qe].transpose(0, 1).numpy(), np.array(on), atol=1e-12)
         np.testing.assert_allclose(lse[:, qs:qe].numpy(), np.array(ln), atol=1e-12)
+
+
+def _scatter_cache(seqs_k, seqs_v, block_size, num_blocks, perm):
+    """Writes each sequence's K/V [n, Hkv, D] into a cache through a block
+    table that hands out the physical blocks in the order `perm`."""
+    hkv, d = seqs_k[0].shape[1:]
+    kc = torch.zeros(num_blocks, block_size, hkv, d, dtype=torch.float64)
+    vc = torch.zeros_like(kc)
+    max_blocks = max((k.shape[0] + block_size - 1) // block_size for k in seqs_k)
+    table = torch.full((len(seqs_k), max(max_blocks, 1)), -1, dtype=torch.int32)
+    nxt = 0
+    for b, (k, v) in enumerate(zip(seqs_k, seqs_v)):
+        for t in range(k.shape[0]):
+            if t % block_size == 0:
+                table[b, t // block_size] = perm[nxt]
+                nxt += 1
+            kc[table[b, t // block_size], t % block_size] = k[t]
+            vc[table[b, t // block_size], t % block_size] = v[t]
+    return kc, vc, table
+
+
+def test_paged_decode_matches_loops():
+    g = torch.Generator().manual_seed(13)
+    lens, hq, hkv, d, bs = [5, 0, 9, 4], 4, 2, 8, 4
+    seqs_k = [torch.randn(n, hkv, d, generator=g, dtype=torch.float64) for n in lens]
+    seqs_v = [torch.randn(n, hkv, d, generator=g, dtype=torch.float64) for n in lens]
+    q = torch.randn(len(lens), hq, d, generator=g, dtype=torch.float64)
+    num_blocks = 8
+    perm = torch.randperm(num_blocks, generator=g).tolist()
+    kc, vc, table = _scatter_cache(seqs_k, seqs_v, bs, num_blocks, perm)
+    o, lse = paged_decode_reference(q, kc, vc, table, torch.tensor(lens, dtype=torch.int32), 0.3)
+    for b, n in enumerate(lens):
+        on, ln = naive_attention(q[b].unsqueeze(1).tolist(), seqs_k[b].transpose(0, 1).tolist(),
+                                 seqs_v[b].transpose(0, 1).tolist(), False, 0.3, group=hq // hkv)
+        if n == 0:
+            assert torch.equal(o[b], torch.zeros(hq, d)) and torch.isinf(lse[b]).all()
+            continue
+        np.testing.assert_allclose(o[b].numpy(), np.array(on)[:, 0], atol=1e-12)
+        np.testing.assert_allclose(lse[b].numpy(), np.array(ln)[:, 0], atol=1e-12)
+
+
+def test_paged_decode_block_permutation():
+    g = torch.Generator().manual_seed(17)
+    lens, hkv, d, bs = [7, 12, 1], 2, 8, 4
+    seqs_k = [torch.randn(n, hkv, d, generator=g, dtype=torch.float64) for n in lens]
+    seqs_v = [torch.randn(n, hkv, d, generator=g, dtype=torch.float64) for n in lens]
+    q = torch.randn(3, 8, d, generator=g, dtype=torch.float64)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    a = paged_decode_reference(q, *_scatter_cache(seqs_k, seqs_v, bs, 8, list(range(8))), sl)
+    b = paged_decode_reference(q, *_scatter_cache(seqs_k, seqs_v, bs, 8, [7, 3, 5, 0, 6, 1, 2, 4]), sl)
+    torch.testing.assert_close(a[0], b[0], atol=1e-14, rtol=0)
+    torch.testing.assert_close(a[1], b[1], atol=1e-14, rtol=0)
 
 
 def test_causal_mask_bottom_right():
