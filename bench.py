@@ -46,6 +46,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
+    ap.add_argument("--workload", default="attention", choices=["attention", "decode"],
+                    help="attention: a BASELINE config (default); decode: a paged-KV decode step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=128,
                     help="(batch, head) slices in the CPU-baseline sample (bounded by memory; ~10 s of CPU work)")
@@ -141,12 +143,120 @@ def cpu_baseline(cfg, inp, n_heads, flops_full, step_kind):
     }
 
 
+DECODE = dict(batch=32, heads_q=32, heads_kv=8, head_dim=128, block_size=16, min_len=1024, max_len=8192, seed=4)
+
+
+def bench_decode(args):
+    """One paged-KV decode step (Llama-3-8B shapes, a batch of 32 sequences
+    with context lengths uniform in [1024, 8192], seed 4, blocks scattered
+    over a shuffled cache pool). HBM-bound: the metric is K/V bytes streamed
+    per second."""
+    import torch
+    from lightserve_amd import _lib
+    from lightserve_amd.kernels.paged_attention import paged_attention_decode
+    from oracle.attention import paged_decode_reference
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    c = DECODE
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(c["seed"])
+    B, Hq, Hkv, D, bs = c["batch"], c["heads_q"], c["heads_kv"], c["head_dim"], c["block_size"]
+    lens = torch.randint(c["min_len"], c["max_len"] + 1, (B,), generator=g)
+    nblk = (lens + bs - 1) // bs
+    num_blocks = int(nblk.sum())
+    perm = torch.randperm(num_blocks, generator=g).to(torch.int32)
+    table = torch.zeros(B, int(nblk.max()), dtype=torch.int32)
+    at = 0
+    for b in range(B):
+        table[b, :nblk[b]] = perm[at:at + int(nblk[b])]
+        at += int(nblk[b])
+    q = (torch.randn(B, Hq, D, generator=g) * 0.5).to(torch.bfloat16)
+    kc = (torch.randn(num_blocks, bs, Hkv, D, generator=g) * 0.5).to(torch.bfloat16)
+    vc = torch.randn(num_blocks, bs, Hkv, D, generator=g).to(torch.bfloat16)
+    qd, kd, vd, td = q.to(dev), kc.to(dev), vc.to(dev), table.to(dev)
+    sl = lens.to(torch.int32).to(dev)
+    max_len = int(lens.max())
+
+    def step():
+        return paged_attention_decode(qd, kd, vd, td, sl, max_seq_len=max_len, return_lse=True)
+
+    o, lse = step()
+    torch.cuda.synchronize()
+    worst = {"o": [0.0, 0.0], "lse": [0.0, 0.0]}
+    for b in (0, B - 1):  # oracle check of two sequences
+        o_ref, lse_ref = paged_decode_reference(q[b:b + 1], kc, vc, table[b:b + 1], lens[b:b + 1].to(torch.int32))
+        for name, got, ref in (("o", o[b:b + 1].cpu(), o_ref), ("lse", lse[b:b + 1].cpu(), lse_ref)):
+            err = (got.double() - ref.double()).abs()
+            worst[name] = [max(worst[name][0], err.max().item()), max(worst[name][1], err.mean().item())]
+    parity = {n: {"max_abs": float(f"{v[0]:.3e}"), "mean_abs": float(f"{v[1]:.3e}")} for n, v in worst.items()}
+    parity_ok = worst["o"][0] <= 2e-2 and worst["o"][1] <= 2e-3 and worst["lse"][0] <= 1e-3
+
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, e in ev:
+        a.record(stream)
+        step()
+        e.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = sum(a.elapsed_time(e) for a, e in ev) / len(ev)
+    tokens = int(lens.sum())
+    kv_bytes = tokens * Hkv * D * 2 * 2          # K and V rows, bf16
+    other_bytes = B * Hq * D * 2 * 2 + B * Hq * 4 + table.numel() * 4 + B * 4  # q, o, lse, tables, lens
+    alg_bytes = kv_bytes + other_bytes
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "paged-KV decode attention: algorithmic HBM GB/s (K/V streamed), 1 GPU",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": f"synthetic, seeded (seed {c['seed']}), cache resident in HBM",
+        "config": {"workload": (f"decode: B={B} Hq={Hq} Hkv={Hkv} D={D} block_size={bs} "
+                                f"context uniform in [{c['min_len']}, {c['max_len']}] ({tokens} cached tokens)"),
+                   "bytes_per_step": alg_bytes},
+        "wall_s_timed": round(wall, 4),
+        "parity": {"ok": parity_ok, **parity},
+        "roofline": {"kernel": "fa_decode_split_kernel (+ fa_decode_combine_kernel)", "bound": "hbm",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("fa_decode_split_kernel", "decode"),
+                     "bytes_per_launch": alg_bytes, "avg_launch_ms": round(ms, 5)},
+    }
+    if not args.no_cpu_baseline:
+        # the oracle's gather + closed form in fp32 on the host cores, on a sample of sequences
+        n_cpu = 8
+        t_start = time.perf_counter()
+        reps = 0
+        while True:
+            paged_decode_reference(q[:n_cpu], kc, vc, table[:n_cpu], lens[:n_cpu].to(torch.int32), dtype=torch.float32)
+            reps += 1
+            if time.perf_counter() - t_start > 5.0:
+                break
+        t = (time.perf_counter() - t_start) / reps
+        sample_bytes = int(lens[:n_cpu].sum()) * Hkv * D * 2 * 2
+        result["cpu_baseline"] = {
+            "value": round(sample_bytes / t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"oracle paged_decode_reference (gather + closed form, fp32) on {n_cpu} of {B} sequences, "
+                       f"{reps} repetitions in {time.perf_counter() - t_start:.1f} s"),
+        }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload == "decode":
+        bench_decode(args)
+        return
     import torch
     from lightserve_amd import _lib
     from lightserve_amd.kernels.flash_attention_backward import (_flash_attention_backward,

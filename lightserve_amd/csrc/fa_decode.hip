@@ -29,12 +29,51 @@ namespace lsfa {
 
 constexpr float kDecLn2 = 0.6931471805599453f;
 
+// Sum over the DP/8 lanes that hold one token's row, left in every one of
+// them, with DPP row operations (VALU, no LDS round trip). 16-lane groups:
+// rotations by 8, 4, 2, 1 within the row. 8-lane groups: mirror within the
+// half row, then swaps within quads.
+__device__ __forceinline__ float dpp_add(float x, int ctrl_sel) {
+  int v = __float_as_int(x);
+  int r;
+  switch (ctrl_sel) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;  // row_ror:8
+    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false); break;  // row_ror:4
+    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x122, 0xf, 0xf, false); break;  // row_ror:2
+    case 3: r = __builtin_amdgcn_update_dpp(0, v, 0x121, 0xf, 0xf, false); break;  // row_ror:1
+    case 4: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break;  // row_half_mirror
+    case 5: r = __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false); break;   // quad_perm [2,3,0,1]
+    default: r = __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false); break;  // quad_perm [1,0,3,2]
+  }
+  return x + __int_as_float(r);
+}
+
 template <int DP>
 __device__ __forceinline__ float group_sum(float x) {
-  // sum over the DP/8 lanes that hold one token's row
-#pragma unroll
-  for (int m = DP / 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, DP / 8);
+  if constexpr (DP == 128) {
+    x = dpp_add(x, 0);
+    x = dpp_add(x, 1);
+    x = dpp_add(x, 2);
+    x = dpp_add(x, 3);
+  } else {
+    x = dpp_add(x, 4);
+    x = dpp_add(x, 5);
+    x = dpp_add(x, 6);
+  }
   return x;
+}
+
+__device__ __forceinline__ float dot2(bf16x2 a, bf16x2 b, float c) { return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false); }
+__device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+// a . b over 8 bf16/f16 elements (fp32 accumulate). The pairs are taken with
+// explicit shuffles: bit-casting single 32-bit lanes of a u32x4 to a 2-element
+// vector was miscompiled (every pair read the same register).
+template <typename X8>
+__device__ __forceinline__ float dot8(const X8& a, const X8& b) {
+  float d = dot2(__builtin_shufflevector(a, a, 0, 1), __builtin_shufflevector(b, b, 0, 1), 0.f);
+  d = dot2(__builtin_shufflevector(a, a, 2, 3), __builtin_shufflevector(b, b, 2, 3), d);
+  d = dot2(__builtin_shufflevector(a, a, 4, 5), __builtin_shufflevector(b, b, 4, 5), d);
+  return dot2(__builtin_shufflevector(a, a, 6, 7), __builtin_shufflevector(b, b, 6, 7), d);
 }
 
 template <typename T, int DP, int G>
@@ -65,21 +104,20 @@ __global__ __launch_bounds__(256) void fa_decode_split_kernel(const DecodeParams
   const int32_t* table = p.block_tables + (int64_t)b * p.sbt + first_slot;
   for (int i = tid; i < n_slots; i += 256) s_blk[i] = table[i];
 
-  // q of the G query heads of this KV head, dims 8c..8c+7, pre-scaled to
-  // log2 units.
-  float qf[G][8];
+  // q of the G query heads of this KV head, dims 8c..8c+7 (scores via
+  // v_dot2, fp32 accumulate; the scale is applied after).
+  X8 qp[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int h = hk * G + g;
     u32x4 raw = {0, 0, 0, 0};
     if (8 * c < p.D) raw = ldg16((const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh + 8 * c);
-    const X8 v = __builtin_bit_cast(X8, raw);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qf[g][e] = (float)v[e] * p.scale_log2;
+    qp[g] = __builtin_bit_cast(X8, raw);
   }
+  const float sl2 = p.scale_log2;
   __syncthreads();
 
-  float m[G], l[G], acc[G][8];
+  float m[G], l[G], acc[G][8];  // m in log2 units of scaled scores
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
@@ -93,37 +131,34 @@ __global__ __launch_bounds__(256) void fa_decode_split_kernel(const DecodeParams
   const bool col_ok = 8 * c < p.D;
   const int bmask = (1 << p.block_shift) - 1;
 
-  // Every lane group (wave, tq) walks its own tokens: scores of a chunk of
-  // CH tokens, one offset update, then the weighted V sum.
-  for (int tb = t0 + wave * TPW + tq; tb < t1; tb += CH * TPI) {
-    float s[CH][G];
-    X8 vv[CH];
-    bool ok[CH];
+  // Every lane group (wave, tq) walks its own tokens in chunks of CH; the
+  // loads of the next chunk are in flight while the current one is used.
+  auto load_chunk = [&](int tb, u32x4* kr, u32x4* vr) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int t = tb + u * TPI;
-      ok[u] = t < t1;
-      u32x4 kr = {0, 0, 0, 0}, vr = {0, 0, 0, 0};
-      const int blk = ok[u] ? s_blk[(t >> p.block_shift) - first_slot] : 0;
-      if (ok[u] && col_ok && (unsigned)blk < (unsigned)p.num_blocks) {
+      kr[u] = u32x4{0, 0, 0, 0};
+      vr[u] = u32x4{0, 0, 0, 0};
+      const int blk = t < t1 ? s_blk[(t >> p.block_shift) - first_slot] : -1;
+      if (t < t1 && col_ok && (unsigned)blk < (unsigned)p.num_blocks) {
         const int slot = t & bmask;
-        kr = ldg16(kbase + (int64_t)blk * p.skb + (int64_t)slot * p.sks);
-        vr = ldg16(vbase + (int64_t)blk * p.svb + (int64_t)slot * p.svs);
-      }
-      const X8 kv = __builtin_bit_cast(X8, kr);
-      vv[u] = __builtin_bit_cast(X8, vr);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qf[g][e], (float)kv[e], d);
-        s[u][g] = d;
+        kr[u] = ldg16(kbase + (int64_t)blk * p.skb + (int64_t)slot * p.sks);
+        vr[u] = ldg16(vbase + (int64_t)blk * p.svb + (int64_t)slot * p.svs);
       }
     }
+  };
+  auto use_chunk = [&](int tb, const u32x4* kr, const u32x4* vr) {
+    float s[CH][G];
 #pragma unroll
-    for (int u = 0; u < CH; ++u)
+    for (int u = 0; u < CH; ++u) {
+      const bool ok = tb + u * TPI < t1;
+      const X8 kx = __builtin_bit_cast(X8, kr[u]);
 #pragma unroll
-      for (int g = 0; g < G; ++g) s[u][g] = ok[u] ? group_sum<DP>(s[u][g]) : -INFINITY;
+      for (int g = 0; g < G; ++g) {
+        const float d = group_sum<DP>(dot8(qp[g], kx));
+        s[u][g] = ok ? d * sl2 : -INFINITY;
+      }
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float mx = m[g];
@@ -136,14 +171,34 @@ __global__ __launch_bounds__(256) void fa_decode_split_kernel(const DecodeParams
         for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
         m[g] = mx;
       }
+    }
 #pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const float pv = ok[u] ? fast_exp2(s[u][g] - m[g]) : 0.f;
+    for (int u = 0; u < CH; ++u) {
+      const X8 vv = __builtin_bit_cast(X8, vr[u]);
+      float vf[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vf[e] = (float)vv[e];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pv = fast_exp2(s[u][g] - m[g]);  // exp2(-inf) = 0 past the end
         l[g] += pv;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv, (float)vv[u][e], acc[g][e]);
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv, vf[e], acc[g][e]);
       }
     }
+  };
+  u32x4 ka[CH], va[CH], kb[CH], vb[CH];
+  int tb = t0 + wave * TPW + tq;
+  if (tb < t1) load_chunk(tb, ka, va);
+  while (tb < t1) {
+    const int tn = tb + CH * TPI;
+    if (tn < t1) load_chunk(tn, kb, vb);
+    use_chunk(tb, ka, va);
+    if (tn >= t1) break;
+    const int tn2 = tn + CH * TPI;
+    if (tn2 < t1) load_chunk(tn2, ka, va);
+    use_chunk(tn, kb, vb);
+    tb = tn2;
   }
 
   // Merge the wave's TPW lane groups (lanes with equal c) with shuffles, then
