@@ -117,8 +117,11 @@ DecodeSplit decode_split(const lsfa_decode_args* a) {
   DecodeSplit d;
   const int maxs = std::max(a->max_seq_len, 0);
   const long long units = std::max(1LL, (long long)a->batch * a->heads_kv);
+  // Splits of about 512 tokens while fewer than ~16 workgroups per CU exist:
+  // sequence lengths vary, and short splits keep the longest sequences from
+  // setting the tail.
   long long ns = 1;
-  if (units < 1024 && maxs > 256) ns = std::min<long long>((1024 + units - 1) / units, (maxs + 255) / 256);
+  if (units < 4096 && maxs > 512) ns = std::min<long long>((4096 + units - 1) / units, (maxs + 511) / 512);
   long long st = (maxs + ns - 1) / ns;
   st = std::max(64LL, (st + 63) / 64 * 64);
   const int shift = std::max(0, log2_exact(std::max(1, a->block_size)));
