@@ -143,6 +143,20 @@ def cpu_baseline(cfg, inp, n_heads, flops_full, step_kind):
     }
 
 
+def calibration_copy(dev, mib):
+    """A plain device copy of known size (reads and writes exactly mib MiB),
+    the reference kernel for scaling FETCH_SIZE / WRITE_SIZE counters."""
+    if mib <= 0:
+        return
+    import torch
+    src = torch.empty(mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 DECODE = dict(batch=32, heads_q=32, heads_kv=8, head_dim=128, block_size=16, min_len=1024, max_len=8192, seed=4)
 
 
@@ -194,6 +208,7 @@ def bench_decode(args):
     parity = {n: {"max_abs": float(f"{v[0]:.3e}"), "mean_abs": float(f"{v[1]:.3e}")} for n, v in worst.items()}
     parity_ok = worst["o"][0] <= 2e-2 and worst["o"][1] <= 2e-3 and worst["lse"][0] <= 1e-3
 
+    calibration_copy(dev, args.calibrate_copy)
     for _ in range(args.warmup):
         step()
     stream = torch.cuda.current_stream(dev)
@@ -331,14 +346,7 @@ def main():
         if bwd is not None:
             bwd(o, lse)
 
-    if args.calibrate_copy > 0:
-        # A plain copy of known size: reads and writes exactly MIB MiB each.
-        src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    calibration_copy(dev, args.calibrate_copy)
 
     for _ in range(args.warmup):
         step()
