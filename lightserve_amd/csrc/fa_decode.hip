@@ -23,6 +23,7 @@
 //     groups merge with shuffles, waves through LDS.
 //   fa_decode_combine_kernel: when a sequence is split, merges the splits'
 //     normalised partial outputs with their logsumexps.
+// K/V rows are read with nontemporal loads: each byte is used once per step.
 #include "fa_common.hpp"
 
 namespace lsfa {
@@ -142,8 +143,8 @@ __global__ __launch_bounds__(256) void fa_decode_split_kernel(const DecodeParams
       const int blk = t < t1 ? s_blk[(t >> p.block_shift) - first_slot] : -1;
       if (t < t1 && col_ok && (unsigned)blk < (unsigned)p.num_blocks) {
         const int slot = t & bmask;
-        kr[u] = ldg16(kbase + (int64_t)blk * p.skb + (int64_t)slot * p.sks);
-        vr[u] = ldg16(vbase + (int64_t)blk * p.svb + (int64_t)slot * p.svs);
+        kr[u] = __builtin_nontemporal_load((const u32x4*)(kbase + (int64_t)blk * p.skb + (int64_t)slot * p.sks));
+        vr[u] = __builtin_nontemporal_load((const u32x4*)(vbase + (int64_t)blk * p.svb + (int64_t)slot * p.svs));
       }
     }
   };
@@ -261,21 +262,55 @@ __global__ __launch_bounds__(256) void fa_decode_split_kernel(const DecodeParams
 
 // Merges the splits of one (sequence, query head): o = sum_s w_s o_s / sum_s
 // w_s with w_s = 2^(lse_s - max lse); lse = max + log2(sum w) (log2 units in
-// the workspace, natural log in the output).
+// the workspace, natural log in the output). The splits' lse values are
+// staged in LDS (batches of kCombineBatch, one load per thread, merged with a
+// running max), and the partial rows are read eight splits at a time so that
+// their loads are in flight together.
+constexpr int kCombineBatch = 512;
+
 template <typename T, int DP>
 __global__ __launch_bounds__(DP) void fa_decode_combine_kernel(const DecodeParams p) {
+  constexpr int U = 8;
+  __shared__ float s_w[kCombineBatch];
+  __shared__ float s_red[DP / 64];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int64_t row0 = ((int64_t)b * p.Hq + h) * p.num_splits;
   const int seq = min(max(p.seq_lens[b], 0), min(p.max_seq_len, p.max_blocks << p.block_shift));
   const int ns = min(p.num_splits, (seq + p.split_tokens - 1) / p.split_tokens);
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, p.lse_part[row0 + s]);
-  float W = 0.f, O = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < ns; ++s) {
-      const float w = fast_exp2(p.lse_part[row0 + s] - M);
-      W += w;
-      O += w * p.o_part[(row0 + s) * DP + d];
+  float M = -INFINITY, W = 0.f, O = 0.f;
+  for (int c0 = 0; c0 < ns; c0 += kCombineBatch) {
+    const int cn = min(kCombineBatch, ns - c0);
+    __syncthreads();  // s_w and s_red of the previous batch are consumed
+    float mx = -INFINITY;
+    for (int s = d; s < cn; s += DP) {
+      const float v = p.lse_part[row0 + c0 + s];
+      s_w[s] = v;
+      mx = fmaxf(mx, v);
+    }
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk));
+    if ((d & 63) == 0) s_red[d >> 6] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < DP / 64; ++w) mx = fmaxf(mx, s_red[w]);
+    const float Mn = fmaxf(M, mx);
+    if (Mn == -INFINITY) continue;  // nothing visible so far
+    const float a = fast_exp2(M - Mn);  // 0 while M is still -inf
+    W *= a;
+    O *= a;
+    M = Mn;
+    for (int s0 = 0; s0 < cn; s0 += U) {
+      float o[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) o[u] = s0 + u < cn ? p.o_part[(row0 + c0 + s0 + u) * DP + d] : 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (s0 + u < cn) {
+          const float w = fast_exp2(s_w[s0 + u] - M);
+          W += w;
+          O += w * o[u];
+        }
+      }
     }
   }
   if (d < p.D) ((T*)p.o)[(int64_t)b * p.sob + (int64_t)h * p.soh + d] = (T)(W > 0.f ? O / W : 0.f);

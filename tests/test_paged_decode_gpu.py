@@ -76,6 +76,15 @@ def test_decode_long_split(gpu, lens):
     _check(*_make_case(lens, 8, 1, 128, 16, torch.bfloat16, gpu, seed=len(lens)), f"split {lens}")
 
 
+def test_decode_more_splits_than_one_combine_batch(gpu):
+    """Block size 1 caps a split at 448 tokens (511 table slots in LDS), so
+    240000 tokens make 536 splits: more than the 512 logsumexps the combine
+    kernel stages at a time, which exercises its running-max merge across
+    batches."""
+    print("case decode 240000 tokens, block size 1 (536 splits)", flush=True)
+    _check(*_make_case([240000], 2, 1, 64, 1, torch.bfloat16, gpu, seed=11), "536 splits")
+
+
 def test_decode_many_sequences_unsplit(gpu):
     """Enough (sequence, kv head) pairs to fill the GPU: no split."""
     g = torch.Generator().manual_seed(3)
