@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define LSFA_ABI_VERSION 3
+#define LSFA_ABI_VERSION 4
 
 typedef enum {
   LSFA_DTYPE_FP32 = 0,
@@ -177,6 +177,48 @@ typedef struct {
   float sm_scale;
 } lsfa_decode_args;
 
+/* Rotary position embedding, applied in place to q and k in one launch.
+ * Replaces the reference's apply_rope (model/minimal_llama.py:163-173):
+ * for each token at position pos and each head,
+ *   x[..., :D/2] <- x1 * cos[pos, :D/2] - x2 * sin[pos, :D/2]
+ *   x[..., D/2:] <- x2 * cos[pos, D/2:] + x1 * sin[pos, D/2:]
+ * with x1 = x[..., :D/2], x2 = x[..., D/2:] (x * cos + rotate_half(x) * sin),
+ * computed in fp32 and rounded once to the tensor's dtype.
+ *   q          [batch, heads_q, seqlen, head_dim], element strides (b, h, n, d)
+ *   k          [batch, heads_kv, seqlen, head_dim], or NULL with heads_kv = 0
+ *   cos, sin   [max_pos, head_dim] rows in q's dtype (the reference's
+ *              precompute_rope tables, model/minimal_llama.py:144-156);
+ *              table_stride = elements between rows
+ *   positions  int32 [batch]: position of each sequence's first token, or
+ *              NULL for 0 (prefill from the start); token n sits at
+ *              positions[b] + n, clamped on the device to [0, max_pos)
+ *   cu_seqlens int32 [batch + 1] or NULL: packed [total_tokens, heads,
+ *              head_dim] tensors as in lsfa_fwd_args (stride[0] ignored,
+ *              stride[1] head, stride[2] token); seqlen = max tokens per
+ *              sequence
+ * head_dim must be even with head_dim/2 a multiple of 8 (bf16/fp16) or 4
+ * (fp32) elements; stride[3] == 1, other strides multiples of 8 (bf16/fp16)
+ * or 4 (fp32) elements, 16-byte aligned pointers. */
+typedef struct {
+  void* q;
+  void* k;
+  const void* cos;
+  const void* sin;
+  const int32_t* positions;
+  const int32_t* cu_seqlens;
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t table_stride;
+  int32_t dtype;
+  int32_t batch;
+  int32_t seqlen;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t head_dim;
+  int32_t max_pos;
+  int32_t reserved;
+} lsfa_rope_args;
+
 /* ABI version of the loaded library (LSFA_ABI_VERSION). */
 int lsfa_abi_version(void);
 
@@ -216,6 +258,12 @@ int lsfa_decode_workspace_size(const lsfa_decode_args* args, uint64_t* bytes);
  * seq_lens[b] cached tokens (and lse if requested). No reference
  * counterpart (see lsfa_decode_args). */
 int lsfa_decode(const lsfa_decode_args* args, void* stream);
+
+/* Host-only validation of RoPE arguments; never touches the GPU. */
+int lsfa_rope_check(const lsfa_rope_args* args);
+
+/* In-place RoPE of q and k (see lsfa_rope_args). */
+int lsfa_rope(const lsfa_rope_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ import torch
 
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
 TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}
@@ -22,7 +22,8 @@ STATUS = {0: "LSFA_OK", -1: "LSFA_ERR_INVALID", -2: "LSFA_ERR_UNSUPPORTED", -3: 
 
 EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "lsfa_fwd",
                     "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd",
-                    "lsfa_decode_check", "lsfa_decode_workspace_size", "lsfa_decode")
+                    "lsfa_decode_check", "lsfa_decode_workspace_size", "lsfa_decode",
+                    "lsfa_rope_check", "lsfa_rope")
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -84,6 +85,18 @@ _lock = threading.Lock()
 _lib = None
 
 
+class RopeArgs(ctypes.Structure):
+    """Mirror of lsfa_rope_args."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+        ("positions", ctypes.c_void_p), ("cu_seqlens", ctypes.c_void_p),
+        ("q_stride", _i64x4), ("k_stride", _i64x4), ("table_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32),
+        ("heads_q", ctypes.c_int32), ("heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("max_pos", ctypes.c_int32), ("reserved", ctypes.c_int32),
+    ]
+
+
 def library_path():
     return _LIB_PATH
 
@@ -106,11 +119,12 @@ def load():
         lib.lsfa_last_error.restype = ctypes.c_char_p
         lib.lsfa_last_error.argtypes = []
         for name, struct in (("lsfa_fwd_check", FwdArgs), ("lsfa_bwd_check", BwdArgs),
-                             ("lsfa_decode_check", DecodeArgs)):
+                             ("lsfa_decode_check", DecodeArgs), ("lsfa_rope_check", RopeArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct)]
-        for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_decode", DecodeArgs)):
+        for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_decode", DecodeArgs),
+                             ("lsfa_rope", RopeArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
@@ -166,6 +180,16 @@ def decode_workspace_size(args):
 
 def decode(args, stream):
     _raise_on(load().lsfa_decode(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_decode")
+
+
+def rope_check(args):
+    """Host-only validation (no GPU access); returns (status, message)."""
+    rc = load().lsfa_rope_check(ctypes.byref(args))
+    return rc, load().lsfa_last_error().decode(errors="replace")
+
+
+def rope(args, stream):
+    _raise_on(load().lsfa_rope(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_rope")
 
 
 def fwd(args, stream):

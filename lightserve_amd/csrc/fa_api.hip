@@ -16,6 +16,7 @@ hipError_t bwd_mfma(const BwdParams& p, bool is_bf16, int dp, bool causal, hipSt
 hipError_t fwd_f32(const FwdParams& p, int dp, bool causal, bool varlen, float scale, hipStream_t s);
 hipError_t bwd_f32(const BwdParams& p, int dp, bool causal, hipStream_t s);
 hipError_t decode_gqa(const DecodeParams& p, bool is_bf16, int dp, hipStream_t s);
+hipError_t rope_inplace(const RopeParams& p, int dtype, hipStream_t s);
 }  // namespace lsfa
 
 namespace {
@@ -372,6 +373,62 @@ int lsfa_decode(const lsfa_decode_args* a, void* stream) {
   hipError_t e = lsfa::decode_gqa(p, a->dtype == LSFA_DTYPE_BF16, padded_decode_dim(a->head_dim),
                                   reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int lsfa_rope_check(const lsfa_rope_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  if (a->dtype != LSFA_DTYPE_FP32 && a->dtype != LSFA_DTYPE_FP16 && a->dtype != LSFA_DTYPE_BF16)
+    return fail(LSFA_ERR_INVALID, "unknown dtype %d", a->dtype);
+  if (a->batch < 0 || a->seqlen < 0 || a->heads_q < 0 || a->heads_kv < 0 || a->max_pos < 0)
+    return fail(LSFA_ERR_INVALID, "negative size (batch=%d seqlen=%d heads_q=%d heads_kv=%d max_pos=%d)",
+                a->batch, a->seqlen, a->heads_q, a->heads_kv, a->max_pos);
+  const int vec = a->dtype == LSFA_DTYPE_FP32 ? 4 : 8;
+  if (a->head_dim <= 0 || a->head_dim % (2 * vec) != 0 || a->head_dim > 1024)
+    return fail(LSFA_ERR_UNSUPPORTED, "rope head_dim must be a multiple of %d in %d..1024 (got %d)", 2 * vec,
+                2 * vec, a->head_dim);
+  if (a->batch == 0 || a->seqlen == 0 || a->heads_q + a->heads_kv == 0) return ok();
+  if (a->max_pos <= 0) return fail(LSFA_ERR_INVALID, "max_pos must be positive");
+  if (!a->cos || !a->sin) return fail(LSFA_ERR_INVALID, "cos and sin must be non-NULL");
+  if (a->heads_q > 0 && !a->q) return fail(LSFA_ERR_INVALID, "q is NULL with heads_q > 0");
+  if (a->heads_kv > 0 && !a->k) return fail(LSFA_ERR_INVALID, "k is NULL with heads_kv > 0");
+  if (a->table_stride < a->head_dim || a->table_stride % vec != 0)
+    return fail(LSFA_ERR_UNSUPPORTED, "table_stride %lld must be >= head_dim and a multiple of %d",
+                (long long)a->table_stride, vec);
+  if (!aligned16(a->cos) || !aligned16(a->sin)) return fail(LSFA_ERR_UNSUPPORTED, "cos/sin must be 16-byte aligned");
+  const bool varlen = a->cu_seqlens != nullptr;
+  for (int t = 0; t < 2; ++t) {
+    const int64_t* st = t == 0 ? a->q_stride : a->k_stride;
+    const void* ptr = t == 0 ? a->q : a->k;
+    if ((t == 0 ? a->heads_q : a->heads_kv) == 0) continue;
+    const char* name = t == 0 ? "q" : "k";
+    if (st[3] != 1) return fail(LSFA_ERR_UNSUPPORTED, "%s: head-dim stride must be 1 (got %lld)", name, (long long)st[3]);
+    for (int i = varlen ? 1 : 0; i < 3; ++i)
+      if (st[i] % vec != 0)
+        return fail(LSFA_ERR_UNSUPPORTED, "%s: stride[%d]=%lld is not a multiple of %d elements", name, i,
+                    (long long)st[i], vec);
+    if (!aligned16(ptr)) return fail(LSFA_ERR_UNSUPPORTED, "%s: base pointer is not 16-byte aligned", name);
+  }
+  return ok();
+}
+
+int lsfa_rope(const lsfa_rope_args* a, void* stream) {
+  int rc = lsfa_rope_check(a);
+  if (rc) return rc;
+  if (a->batch == 0 || a->seqlen == 0 || a->heads_q + a->heads_kv == 0) return ok();
+  lsfa::RopeParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = a->q; p.k = a->k; p.cos = a->cos; p.sin = a->sin;
+  p.pos0 = a->positions; p.cu_seqlens = a->cu_seqlens;
+  for (int i = 0; i < 4; ++i) {
+    p.sq[i] = a->q_stride[i];
+    p.sk[i] = a->k_stride[i];
+  }
+  p.table_stride = a->table_stride;
+  p.B = a->batch; p.N = a->seqlen; p.Hq = a->heads_q; p.Hkv = a->heads_kv; p.D = a->head_dim;
+  p.max_pos = a->max_pos;
+  hipError_t e = lsfa::rope_inplace(p, a->dtype, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "rope launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

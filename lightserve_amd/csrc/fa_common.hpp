@@ -202,6 +202,22 @@ struct DecodeParams {
   float scale_log2;       // sm_scale * log2(e)
 };
 
+// In-place rotary embedding of q [B, Hq, N, D] and k [B, Hkv, N, D]
+// (element strides in b, h, n, d order; packed [tokens, h, d] when
+// cu_seqlens is set, then strides[0] is unused and strides[2] is the token
+// stride). cos/sin: [max_pos, D] rows of the input dtype.
+struct RopeParams {
+  void* q;
+  void* k;                     // null when Hkv == 0
+  const void* cos;
+  const void* sin;
+  const int32_t* pos0;         // [B] position of each sequence's first token, or null (0)
+  const int32_t* cu_seqlens;   // [B + 1] or null
+  int64_t sq[4], sk[4];
+  int64_t table_stride;
+  int B, N, Hq, Hkv, D, max_pos;
+};
+
 // Maps the 1-D launch index to (batch*head, tile). Workgroups are handed to
 // the 8 XCDs round-robin by launch index, so consecutive launch indices are
 // spread so that each XCD owns a contiguous run of heads (their K/V stay in

@@ -12,6 +12,8 @@ Contents
                 tiled forward/backward loops, varlen/GQA, paged-KV decode,
                 and a pure-Python loop version for tiny inputs.
   inputs.py     the seeded input recipe of the five BASELINE configurations.
+  model.py      the reference's model forward in plain torch (RoPE tables and
+                rotation, RMSNorm, reference_llama_forward, with GQA).
 
 How each function is pinned (tests/test_oracle.py):
   attention_reference   pure-Python loops (golden fixtures under tests/golden),
@@ -23,6 +25,8 @@ How each function is pinned (tests/test_oracle.py):
   paged_decode_reference  pure-Python loops over a hand-built cache, the
                         dense closed form through an identity block table,
                         and invariance under a permutation of the blocks.
+  model.apply_rope      RoPE as an element-by-element rotation (tests/test_oracle_model.py).
+  model.reference_llama_forward  a pure-Python float64 one-layer forward.
 Every function has at least one check that a planted mistake (a dropped
 scale, a transposed operand, a wrong mask offset) fails.
 """

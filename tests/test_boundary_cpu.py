@@ -106,9 +106,11 @@ def test_struct_layout_matches_header(built_library):
     if cc is None:
         pytest.skip("no host C compiler")
     src = ('#include <stdio.h>\n#include <stddef.h>\n#include "lightserve_fa.h"\n'
-           'int main(void){printf("%zu %zu %zu %zu %zu %zu %zu\\n", sizeof(lsfa_fwd_args), sizeof(lsfa_bwd_args),'
-           ' offsetof(lsfa_fwd_args, sm_scale), offsetof(lsfa_bwd_args, sm_scale), sizeof(lsfa_decode_args),'
-           ' offsetof(lsfa_decode_args, block_table_stride), offsetof(lsfa_decode_args, sm_scale)); return 0;}\n')
+           'int main(void){printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(lsfa_fwd_args),'
+           ' sizeof(lsfa_bwd_args), offsetof(lsfa_fwd_args, sm_scale), offsetof(lsfa_bwd_args, sm_scale),'
+           ' sizeof(lsfa_decode_args), offsetof(lsfa_decode_args, block_table_stride),'
+           ' offsetof(lsfa_decode_args, sm_scale), sizeof(lsfa_rope_args), offsetof(lsfa_rope_args, table_stride),'
+           ' offsetof(lsfa_rope_args, max_pos)); return 0;}\n')
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "t.c")
         exe = os.path.join(d, "t")
@@ -117,7 +119,8 @@ def test_struct_layout_matches_header(built_library):
         sizes = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
     assert sizes == [ctypes.sizeof(_lib.FwdArgs), ctypes.sizeof(_lib.BwdArgs),
                      _lib.FwdArgs.sm_scale.offset, _lib.BwdArgs.sm_scale.offset, ctypes.sizeof(_lib.DecodeArgs),
-                     _lib.DecodeArgs.block_table_stride.offset, _lib.DecodeArgs.sm_scale.offset]
+                     _lib.DecodeArgs.block_table_stride.offset, _lib.DecodeArgs.sm_scale.offset,
+                     ctypes.sizeof(_lib.RopeArgs), _lib.RopeArgs.table_stride.offset, _lib.RopeArgs.max_pos.offset]
 
 
 def _fwd_args(**kw):
@@ -217,3 +220,39 @@ def test_abi_backward_workspace(built_library):
     # fp32 needs only the (L, delta) pairs
     args.dtype = _lib.DTYPE_FP32
     assert _lib.bwd_workspace_size(args) == rows * 8
+
+
+def _rope_args(**kw):
+    st = _lib._i64x4(4 * 16 * 64, 64, 4 * 64, 1)  # [B, N, H, D] storage viewed as (b, h, n, d)
+    base = dict(q=4096, k=8192, cos=12288, sin=16384, positions=None, cu_seqlens=None, q_stride=st,
+                k_stride=st, table_stride=64, dtype=_lib.DTYPE_BF16, batch=2, seqlen=16, heads_q=4,
+                heads_kv=4, head_dim=64, max_pos=128, reserved=0)
+    base.update(kw)
+    return _lib.RopeArgs(**base)
+
+
+def test_abi_rope_validation(built_library):
+    """Host-only validation of lsfa_rope (fake, never dereferenced pointers)."""
+    assert _lib.rope_check(_rope_args())[0] == 0
+    rc, msg = _lib.rope_check(_rope_args(dtype=9))
+    assert rc == -1 and "dtype" in msg
+    rc, msg = _lib.rope_check(_rope_args(head_dim=24))  # half of 24 is not a multiple of 8
+    assert rc == -2 and "head_dim" in msg
+    assert _lib.rope_check(_rope_args(dtype=_lib.DTYPE_FP32, head_dim=24, table_stride=24))[0] == 0
+    rc, msg = _lib.rope_check(_rope_args(k=None))
+    assert rc == -1 and "k is NULL" in msg
+    assert _lib.rope_check(_rope_args(k=None, heads_kv=0))[0] == 0  # q only
+    rc, msg = _lib.rope_check(_rope_args(cos=None))
+    assert rc == -1 and "cos" in msg
+    rc, msg = _lib.rope_check(_rope_args(table_stride=32))
+    assert rc == -2 and "table_stride" in msg
+    rc, msg = _lib.rope_check(_rope_args(q=4100))
+    assert rc == -2 and "aligned" in msg
+    rc, msg = _lib.rope_check(_rope_args(q_stride=_lib._i64x4(4096, 64, 256, 2)))
+    assert rc == -2 and "stride" in msg
+    rc, msg = _lib.rope_check(_rope_args(max_pos=0))
+    assert rc == -1 and "max_pos" in msg
+    # empty problems are a successful no-op; bad input never reaches the GPU
+    _lib.rope(_rope_args(seqlen=0, q=None, k=None), 0)
+    with pytest.raises(RuntimeError, match="LSFA_ERR_INVALID"):
+        _lib.rope(_rope_args(batch=-1), 0)
