@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define LSFA_ABI_VERSION 4
+#define LSFA_ABI_VERSION 5
 
 typedef enum {
   LSFA_DTYPE_FP32 = 0,
@@ -219,6 +219,31 @@ typedef struct {
   int32_t reserved;
 } lsfa_rope_args;
 
+/* Fused residual add + RMSNorm over the rows of [rows, cols] matrices
+ * (column stride 1; row strides in elements). Replaces the reference's
+ * fused_add_rmsnorm launch (kernels/fused_rmsnorm_residual.py:73-118):
+ *   h   = x + residual            (rounded to the dtype; residual_out <- h)
+ *   out = h * rsqrt(mean(h^2) + eps) * weight   (fp32 statistics, rounded once)
+ * residual = NULL gives plain RMSNorm (h = x); residual_out = NULL skips
+ * writing h. out and residual_out may alias x or residual with the same row
+ * stride (each element is read before it is written, by the same thread).
+ * weight: [cols]. */
+typedef struct {
+  const void* x;
+  const void* residual;
+  const void* weight;
+  void* out;
+  void* residual_out;
+  int64_t x_stride;
+  int64_t residual_stride;
+  int64_t out_stride;
+  int64_t residual_out_stride;
+  int32_t dtype;
+  int32_t rows;
+  int32_t cols;
+  float eps;
+} lsfa_rmsnorm_args;
+
 /* ABI version of the loaded library (LSFA_ABI_VERSION). */
 int lsfa_abi_version(void);
 
@@ -264,6 +289,12 @@ int lsfa_rope_check(const lsfa_rope_args* args);
 
 /* In-place RoPE of q and k (see lsfa_rope_args). */
 int lsfa_rope(const lsfa_rope_args* args, void* stream);
+
+/* Host-only validation of RMSNorm arguments; never touches the GPU. */
+int lsfa_rmsnorm_check(const lsfa_rmsnorm_args* args);
+
+/* Fused residual add + RMSNorm (see lsfa_rmsnorm_args). */
+int lsfa_rmsnorm(const lsfa_rmsnorm_args* args, void* stream);
 
 #ifdef __cplusplus
 }

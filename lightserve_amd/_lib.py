@@ -13,7 +13,7 @@ import torch
 
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
 TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}
@@ -23,7 +23,7 @@ STATUS = {0: "LSFA_OK", -1: "LSFA_ERR_INVALID", -2: "LSFA_ERR_UNSUPPORTED", -3: 
 EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "lsfa_fwd",
                     "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd",
                     "lsfa_decode_check", "lsfa_decode_workspace_size", "lsfa_decode",
-                    "lsfa_rope_check", "lsfa_rope")
+                    "lsfa_rope_check", "lsfa_rope", "lsfa_rmsnorm_check", "lsfa_rmsnorm")
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -97,6 +97,17 @@ class RopeArgs(ctypes.Structure):
     ]
 
 
+class RmsNormArgs(ctypes.Structure):
+    """Mirror of lsfa_rmsnorm_args."""
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("residual", ctypes.c_void_p), ("weight", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("residual_out", ctypes.c_void_p),
+        ("x_stride", ctypes.c_int64), ("residual_stride", ctypes.c_int64), ("out_stride", ctypes.c_int64),
+        ("residual_out_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32), ("eps", ctypes.c_float),
+    ]
+
+
 def library_path():
     return _LIB_PATH
 
@@ -119,12 +130,13 @@ def load():
         lib.lsfa_last_error.restype = ctypes.c_char_p
         lib.lsfa_last_error.argtypes = []
         for name, struct in (("lsfa_fwd_check", FwdArgs), ("lsfa_bwd_check", BwdArgs),
-                             ("lsfa_decode_check", DecodeArgs), ("lsfa_rope_check", RopeArgs)):
+                             ("lsfa_decode_check", DecodeArgs), ("lsfa_rope_check", RopeArgs),
+                             ("lsfa_rmsnorm_check", RmsNormArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct)]
         for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_decode", DecodeArgs),
-                             ("lsfa_rope", RopeArgs)):
+                             ("lsfa_rope", RopeArgs), ("lsfa_rmsnorm", RmsNormArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
@@ -190,6 +202,16 @@ def rope_check(args):
 
 def rope(args, stream):
     _raise_on(load().lsfa_rope(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_rope")
+
+
+def rmsnorm_check(args):
+    """Host-only validation (no GPU access); returns (status, message)."""
+    rc = load().lsfa_rmsnorm_check(ctypes.byref(args))
+    return rc, load().lsfa_last_error().decode(errors="replace")
+
+
+def rmsnorm(args, stream):
+    _raise_on(load().lsfa_rmsnorm(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_rmsnorm")
 
 
 def fwd(args, stream):

@@ -17,6 +17,7 @@ hipError_t fwd_f32(const FwdParams& p, int dp, bool causal, bool varlen, float s
 hipError_t bwd_f32(const BwdParams& p, int dp, bool causal, hipStream_t s);
 hipError_t decode_gqa(const DecodeParams& p, bool is_bf16, int dp, hipStream_t s);
 hipError_t rope_inplace(const RopeParams& p, int dtype, hipStream_t s);
+hipError_t add_rmsnorm(const NormParams& p, int dtype, bool vec, hipStream_t s);
 }  // namespace lsfa
 
 namespace {
@@ -429,6 +430,41 @@ int lsfa_rope(const lsfa_rope_args* a, void* stream) {
   p.max_pos = a->max_pos;
   hipError_t e = lsfa::rope_inplace(p, a->dtype, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "rope launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int lsfa_rmsnorm_check(const lsfa_rmsnorm_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  if (a->dtype != LSFA_DTYPE_FP32 && a->dtype != LSFA_DTYPE_FP16 && a->dtype != LSFA_DTYPE_BF16)
+    return fail(LSFA_ERR_INVALID, "unknown dtype %d", a->dtype);
+  if (a->rows < 0 || a->cols < 0) return fail(LSFA_ERR_INVALID, "negative size (rows=%d cols=%d)", a->rows, a->cols);
+  if (!(a->eps >= 0.f) || !std::isfinite(a->eps)) return fail(LSFA_ERR_INVALID, "eps must be finite and >= 0");
+  if (a->rows == 0 || a->cols == 0) return ok();
+  if (!a->x || !a->weight || !a->out) return fail(LSFA_ERR_INVALID, "x, weight and out must be non-NULL");
+  if (a->x_stride < a->cols || a->out_stride < a->cols || (a->residual && a->residual_stride < a->cols) ||
+      (a->residual_out && a->residual_out_stride < a->cols))
+    return fail(LSFA_ERR_INVALID, "row strides must be at least cols (%d)", a->cols);
+  return ok();
+}
+
+int lsfa_rmsnorm(const lsfa_rmsnorm_args* a, void* stream) {
+  int rc = lsfa_rmsnorm_check(a);
+  if (rc) return rc;
+  if (a->rows == 0 || a->cols == 0) return ok();
+  lsfa::NormParams p;
+  memset(&p, 0, sizeof(p));
+  p.x = a->x; p.residual = a->residual; p.weight = a->weight; p.out = a->out; p.residual_out = a->residual_out;
+  p.sx = a->x_stride; p.sr = a->residual_stride; p.so = a->out_stride; p.sh = a->residual_out_stride;
+  p.rows = a->rows; p.cols = a->cols; p.eps = a->eps;
+  // 16-byte path: width and every row stride a multiple of 16 bytes, aligned
+  // pointers, and the row fits 8 groups per thread.
+  const int vec = a->dtype == LSFA_DTYPE_FP32 ? 4 : 8;
+  bool v = a->cols % vec == 0 && a->cols <= 256 * vec * 8 && a->x_stride % vec == 0 && a->out_stride % vec == 0 &&
+           aligned16(a->x) && aligned16(a->out) && aligned16(a->weight);
+  if (a->residual) v = v && a->residual_stride % vec == 0 && aligned16(a->residual);
+  if (a->residual_out) v = v && a->residual_out_stride % vec == 0 && aligned16(a->residual_out);
+  hipError_t e = lsfa::add_rmsnorm(p, a->dtype, v, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "rmsnorm launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

@@ -218,6 +218,19 @@ struct RopeParams {
   int B, N, Hq, Hkv, D, max_pos;
 };
 
+// Fused residual add + RMSNorm over rows of a [rows, cols] matrix (column
+// stride 1, row strides in elements). residual and residual_out may be null.
+struct NormParams {
+  const void* x;
+  const void* residual;
+  const void* weight;
+  void* out;
+  void* residual_out;
+  int64_t sx, sr, so, sh;
+  int rows, cols;
+  float eps;
+};
+
 // Maps the 1-D launch index to (batch*head, tile). Workgroups are handed to
 // the 8 XCDs round-robin by launch index, so consecutive launch indices are
 // spread so that each XCD owns a contiguous run of heads (their K/V stay in

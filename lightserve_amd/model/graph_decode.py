@@ -31,7 +31,8 @@ import torch.nn.functional as F
 
 from ..kernels.paged_attention import paged_attention_decode
 from ..kernels.rope import apply_rope_
-from .minimal_llama import init_weights, llama3_8b_shape, llama_forward, precompute_rope, rmsnorm
+from ..kernels.fused_rmsnorm_residual import fused_add_rmsnorm
+from .minimal_llama import add_norm, init_weights, llama3_8b_shape, llama_forward, precompute_rope
 
 SEED_TOKEN_ID = 1
 
@@ -139,8 +140,9 @@ class KVCacheDecoder:
             + (pos % self.bs).long()
         lens = pos + 1
         residual = F.embedding(self.tokens, self.w.embed_tokens)  # [B, H]
+        pending = None
         for i, layer in enumerate(self.w.layers):
-            h = rmsnorm(residual, layer.input_layernorm_weight, cfg.rms_eps)
+            h, residual = add_norm(pending, residual, layer.input_layernorm_weight, cfg.rms_eps)
             q = torch.matmul(h, layer.q_proj)
             k = torch.matmul(h, layer.k_proj)
             v = torch.matmul(h, layer.v_proj)
@@ -149,11 +151,12 @@ class KVCacheDecoder:
             self.v_cache[i].view(-1, nkv, hd).index_copy_(0, slot, v.view(B, nkv, hd))
             o = paged_attention_decode(q.view(B, nh, hd), self.k_cache[i], self.v_cache[i], self.block_tables,
                                        lens, max_seq_len=cfg.max_seq_len)
-            residual = residual + torch.matmul(o.view(B, nh * hd), layer.o_proj)
-            h2 = rmsnorm(residual, layer.post_attention_layernorm_weight, cfg.rms_eps)
+            h2, residual = fused_add_rmsnorm(torch.matmul(o.view(B, nh * hd), layer.o_proj), residual,
+                                             layer.post_attention_layernorm_weight, cfg.rms_eps)
             mlp = F.silu(torch.matmul(h2, layer.gate_proj)) * torch.matmul(h2, layer.up_proj)
-            residual = residual + torch.matmul(mlp, layer.down_proj)
-        return torch.matmul(rmsnorm(residual, self.w.norm_weight, cfg.rms_eps), self.w.lm_head)
+            pending = torch.matmul(mlp, layer.down_proj)
+        final, _ = add_norm(pending, residual, self.w.norm_weight, cfg.rms_eps)
+        return torch.matmul(final, self.w.lm_head)
 
     def advance(self, logits):
         """Greedy next token; one more cached token per sequence."""

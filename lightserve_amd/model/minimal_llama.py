@@ -11,9 +11,14 @@ model/cuda_graph_decode.py run against this module unchanged. What differs:
     the reference's MHA shape.
   - RoPE is one HIP launch that rotates q and k in place (lsfa_rope)
     instead of the reference's elementwise tensor ops (:163-173).
+  - Every residual add + RMSNorm is one lsfa_rmsnorm launch
+    (kernels.fused_rmsnorm_residual.fused_add_rmsnorm), as the reference uses
+    its fused kernel (:197-238): a sublayer's output is folded into the
+    residual by the next norm. The first norm has no pending output and is
+    the same kernel without the add (the reference adds a zero tensor).
   - Linear layers are torch matmuls (hipBLASLt) on the reference's [in, out]
-    weights, and RMSNorm is the reference's fp32 formula (:263-266) in torch:
-    those kernels are off the attention path.
+    weights: kernels.tiled_matmul.matmul is the same call behind the
+    reference's argument checks, which the model skips.
 The forward needs no host synchronisation, so it can be captured in a HIP
 graph (model/graph_decode.py).
 """
@@ -24,6 +29,8 @@ import torch
 import torch.nn.functional as F
 
 from ..kernels.flash_attention import flash_attention_forward
+from ..kernels.fused_rmsnorm_residual import fused_add_rmsnorm
+from ..kernels.fused_rmsnorm_residual import rmsnorm as rmsnorm_kernel
 from ..kernels.flash_attention_varlen import flash_attention_varlen_forward
 from ..kernels.rope import apply_rope_
 
@@ -132,11 +139,12 @@ def precompute_rope(config: LlamaConfig, device):
     return cos, sin
 
 
-def rmsnorm(h, weight, eps):
-    """The reference's RMSNorm (model/minimal_llama.py:263-266): fp32 statistics,
-    normalised value cast back before the weight."""
-    h32 = h.float()
-    return (h32 * torch.rsqrt(h32.pow(2).mean(-1, keepdim=True) + eps)).to(h.dtype) * weight
+def add_norm(x, residual, weight, eps):
+    """(rmsnorm(x + residual) * weight, x + residual) in one launch; x None
+    (nothing pending) normalises the residual alone."""
+    if x is None:
+        return rmsnorm_kernel(residual, weight, eps), residual
+    return fused_add_rmsnorm(x, residual, weight, eps)
 
 
 def attention_block(layer, config, normed_2d, B, N, cos, sin, causal, positions=None):
@@ -165,12 +173,13 @@ def llama_forward(weights: LlamaWeights, config: LlamaConfig, input_ids: torch.T
     H = config.hidden_size
     cos, sin = rope_tables if rope_tables is not None else precompute_rope(config, input_ids.device)
     residual = F.embedding(input_ids, weights.embed_tokens).reshape(B * N, H)
+    pending = None  # the last sublayer's output, added to the residual by the next norm
     for layer in weights.layers:
-        normed = rmsnorm(residual, layer.input_layernorm_weight, config.rms_eps)
+        normed, residual = add_norm(pending, residual, layer.input_layernorm_weight, config.rms_eps)
         attn = attention_block(layer, config, normed, B, N, cos, sin, causal)
-        residual = residual + torch.matmul(attn, layer.o_proj)
-        normed2 = rmsnorm(residual, layer.post_attention_layernorm_weight, config.rms_eps)
+        normed2, residual = fused_add_rmsnorm(torch.matmul(attn, layer.o_proj), residual,
+                                              layer.post_attention_layernorm_weight, config.rms_eps)
         mlp = F.silu(torch.matmul(normed2, layer.gate_proj)) * torch.matmul(normed2, layer.up_proj)
-        residual = residual + torch.matmul(mlp, layer.down_proj)
-    final = rmsnorm(residual, weights.norm_weight, config.rms_eps)
+        pending = torch.matmul(mlp, layer.down_proj)
+    final, _ = add_norm(pending, residual, weights.norm_weight, config.rms_eps)
     return torch.matmul(final, weights.lm_head).reshape(B, N, config.vocab_size)

@@ -13,7 +13,8 @@ Contents
                 and a pure-Python loop version for tiny inputs.
   inputs.py     the seeded input recipe of the five BASELINE configurations.
   model.py      the reference's model forward in plain torch (RoPE tables and
-                rotation, RMSNorm, reference_llama_forward, with GQA).
+                rotation, RMSNorm, the fused add + RMSNorm's semantics,
+                reference_llama_forward, with GQA).
 
 How each function is pinned (tests/test_oracle.py):
   attention_reference   pure-Python loops (golden fixtures under tests/golden),
@@ -26,6 +27,9 @@ How each function is pinned (tests/test_oracle.py):
                         dense closed form through an identity block table,
                         and invariance under a permutation of the blocks.
   model.apply_rope      RoPE as an element-by-element rotation (tests/test_oracle_model.py).
+  model.add_rmsnorm_reference  h and out written out by hand per element
+                        (pure-Python sums), with and without the residual; unit
+                        RMS with a unit weight (tests/test_oracle_model.py).
   model.reference_llama_forward  a pure-Python float64 one-layer forward.
 Every function has at least one check that a planted mistake (a dropped
 scale, a transposed operand, a wrong mask offset) fails.

@@ -4,6 +4,7 @@ INFRASTRUCTURE ONLY (see oracle/__init__.py for who may import it).
 Follows model/minimal_llama.py (the reference):
   precompute_rope         :144-156  cos/sin tables [max_seq_len, head_dim], cast to the model dtype
   rotate_half, apply_rope :159-173  x * cos + rotate_half(x) * sin on [B, H, N, D]
+  add_rmsnorm_reference   kernels/fused_rmsnorm_residual.py:40-70 (fused add + RMSNorm)
   reference_llama_forward :254-293  F.linear / SDPA / hand-written RMSNorm, the ground truth
                                     its llama_forward is tested against
                                     (model/tests/test_minimal_llama.py)
@@ -11,11 +12,13 @@ One extension the reference lacks: n_kv_heads < n_heads (grouped-query
 attention), expanded with repeat_interleave over the head axis, the
 reference's own GQA convention (benchmarks/profiling/roofline/measure_roofline.py:94-98).
 
-Pinned in tests/test_oracle.py: apply_rope against the rotation-matrix form
+Pinned in tests/test_oracle_model.py: apply_rope against the rotation-matrix form
 of RoPE built element by element (each pair (d, d + D/2) rotated by the
 angle pos * theta^(-2d/D)), which also fixes the table construction;
 reference_llama_forward's attention against attention_reference, and the
-whole forward against a pure-Python loop on a tiny one-layer model.
+whole forward against a pure-Python loop on a tiny one-layer model;
+add_rmsnorm_reference against per-element Python sums (a planted eps outside
+the square root fails).
 """
 import torch
 import torch.nn.functional as F
@@ -47,6 +50,16 @@ def apply_rope(q, k, cos, sin, n, positions=None):
         c = cos[idx].unsqueeze(1)
         s = sin[idx].unsqueeze(1)
     return q * c + rotate_half(q) * s, k * c + rotate_half(k) * s
+
+
+def add_rmsnorm_reference(x, residual, weight, eps):
+    """The reference's fused add + RMSNorm semantics
+    (kernels/fused_rmsnorm_residual.py:40-70, its test's reference
+    kernels/tests/test_fused_rmsnorm_residual.py:24-29): h = x + residual in
+    the input dtype, fp32 statistics, output rounded once. residual None: h = x."""
+    h = x if residual is None else x + residual
+    var = h.float().pow(2).mean(-1, keepdim=True)
+    return (h.float() * torch.rsqrt(var + eps) * weight.float()).to(x.dtype), h
 
 
 def rmsnorm(h, weight, eps):

@@ -110,7 +110,8 @@ def test_struct_layout_matches_header(built_library):
            ' sizeof(lsfa_bwd_args), offsetof(lsfa_fwd_args, sm_scale), offsetof(lsfa_bwd_args, sm_scale),'
            ' sizeof(lsfa_decode_args), offsetof(lsfa_decode_args, block_table_stride),'
            ' offsetof(lsfa_decode_args, sm_scale), sizeof(lsfa_rope_args), offsetof(lsfa_rope_args, table_stride),'
-           ' offsetof(lsfa_rope_args, max_pos)); return 0;}\n')
+           ' offsetof(lsfa_rope_args, max_pos)); printf("%zu %zu %zu\\n", sizeof(lsfa_rmsnorm_args),'
+           ' offsetof(lsfa_rmsnorm_args, dtype), offsetof(lsfa_rmsnorm_args, eps)); return 0;}\n')
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "t.c")
         exe = os.path.join(d, "t")
@@ -120,7 +121,8 @@ def test_struct_layout_matches_header(built_library):
     assert sizes == [ctypes.sizeof(_lib.FwdArgs), ctypes.sizeof(_lib.BwdArgs),
                      _lib.FwdArgs.sm_scale.offset, _lib.BwdArgs.sm_scale.offset, ctypes.sizeof(_lib.DecodeArgs),
                      _lib.DecodeArgs.block_table_stride.offset, _lib.DecodeArgs.sm_scale.offset,
-                     ctypes.sizeof(_lib.RopeArgs), _lib.RopeArgs.table_stride.offset, _lib.RopeArgs.max_pos.offset]
+                     ctypes.sizeof(_lib.RopeArgs), _lib.RopeArgs.table_stride.offset, _lib.RopeArgs.max_pos.offset,
+                     ctypes.sizeof(_lib.RmsNormArgs), _lib.RmsNormArgs.dtype.offset, _lib.RmsNormArgs.eps.offset]
 
 
 def _fwd_args(**kw):
@@ -256,3 +258,48 @@ def test_abi_rope_validation(built_library):
     _lib.rope(_rope_args(seqlen=0, q=None, k=None), 0)
     with pytest.raises(RuntimeError, match="LSFA_ERR_INVALID"):
         _lib.rope(_rope_args(batch=-1), 0)
+
+
+def _norm_args(**kw):
+    base = dict(x=4096, residual=8192, weight=12288, out=16384, residual_out=20480, x_stride=4096,
+                residual_stride=4096, out_stride=4096, residual_out_stride=4096, dtype=_lib.DTYPE_BF16,
+                rows=8, cols=4096, eps=1e-6)
+    base.update(kw)
+    return _lib.RmsNormArgs(**base)
+
+
+def test_abi_rmsnorm_validation(built_library):
+    """Host-only validation of lsfa_rmsnorm (fake, never dereferenced pointers)."""
+    assert _lib.rmsnorm_check(_norm_args())[0] == 0
+    assert _lib.rmsnorm_check(_norm_args(residual=None, residual_out=None))[0] == 0  # plain RMSNorm
+    assert _lib.rmsnorm_check(_norm_args(cols=17, x=4098))[0] == 0  # odd widths/alignment: scalar path
+    rc, msg = _lib.rmsnorm_check(_norm_args(dtype=5))
+    assert rc == -1 and "dtype" in msg
+    rc, msg = _lib.rmsnorm_check(_norm_args(x=None))
+    assert rc == -1 and "non-NULL" in msg
+    rc, msg = _lib.rmsnorm_check(_norm_args(out_stride=100))
+    assert rc == -1 and "stride" in msg
+    rc, msg = _lib.rmsnorm_check(_norm_args(eps=float("nan")))
+    assert rc == -1 and "eps" in msg
+    _lib.rmsnorm(_norm_args(rows=0, x=None, out=None), 0)  # empty: no-op
+    with pytest.raises(RuntimeError, match="LSFA_ERR_INVALID"):
+        _lib.rmsnorm(_norm_args(rows=-1), 0)
+
+
+def test_rmsnorm_and_matmul_validation_cpu():
+    """The reference's argument checks, in its order, raise AssertionError on
+    CPU tensors before any library call (kernels/tests/test_fused_rmsnorm_residual.py,
+    kernels/tests/test_tiled_matmul.py)."""
+    from lightserve_amd.kernels.fused_rmsnorm_residual import fused_add_rmsnorm
+    from lightserve_amd.kernels.tiled_matmul import matmul
+    x = torch.randn(4, 8)
+    with pytest.raises(AssertionError):
+        fused_add_rmsnorm(x, torch.randn(4, 9), torch.randn(8))
+    with pytest.raises(AssertionError):
+        fused_add_rmsnorm(x, x, torch.randn(9))
+    with pytest.raises(AssertionError):  # CPU tensors
+        fused_add_rmsnorm(x, x, torch.randn(8))
+    with pytest.raises(AssertionError):
+        matmul(torch.randn(2, 3), torch.randn(4, 5))
+    with pytest.raises(AssertionError):  # CPU tensors
+        matmul(torch.randn(2, 3), torch.randn(3, 5))

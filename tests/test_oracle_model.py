@@ -133,3 +133,27 @@ def test_reference_forward_matches_loops(n_kv_heads, causal):
     assert (_forward_loops(w, cfg, ids, causal, eps=1e-1) - want).abs().max() > 1e-2
     if n_kv_heads is not None:
         assert (_forward_loops(w, cfg, ids, causal, round_robin=True) - want).abs().max() > 1e-2
+
+
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_add_rmsnorm_reference_matches_loops(with_residual):
+    """h = x + r; out_j = h_j / sqrt(sum_i h_i^2 / N + eps) * w_j, by hand."""
+    g = torch.Generator().manual_seed(1)
+    x, r = torch.randn(3, 5, generator=g, dtype=torch.float64), torch.randn(3, 5, generator=g, dtype=torch.float64)
+    w = torch.randn(5, generator=g, dtype=torch.float64)
+    eps = 1e-6
+    out, h = om.add_rmsnorm_reference(x, r if with_residual else None, w, eps)
+    for i in range(3):
+        hv = [x[i, j].item() + (r[i, j].item() if with_residual else 0.0) for j in range(5)]
+        s = math.sqrt(sum(v * v for v in hv) / 5 + eps)
+        for j in range(5):
+            assert abs(h[i, j].item() - hv[j]) < 1e-12
+            # statistics in fp32, as the reference computes them (.float())
+            assert abs(out[i, j].item() - hv[j] / s * w[j].item()) < 1e-6 * max(1.0, abs(out[i, j].item()))
+    # planted mistake: eps added outside the square root (visible with a large eps)
+    big, _ = om.add_rmsnorm_reference(x, r if with_residual else None, w, 0.5)
+    bad = h / (h.pow(2).mean(-1, keepdim=True).sqrt() + 0.5) * w
+    assert (bad - big).abs().max() > 1e-2
+    # unit RMS before the weight
+    ones, _ = om.add_rmsnorm_reference(x, r, torch.ones(5, dtype=torch.float64), 0.0)
+    torch.testing.assert_close(ones.pow(2).mean(-1), torch.ones(3, dtype=torch.float64))
