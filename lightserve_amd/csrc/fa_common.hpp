@@ -44,11 +44,17 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
 }
 
 // Transposed 8-byte LDS read (see header comment for the lane mapping).
-__device__ __forceinline__ bf16x4 lds_read_tr(const LDS_AS __bf16* p) {
+// Transposed 4 x 16-bit LDS read. The pointer is __restrict__ so that, once
+// inlined, the read carries its own alias scope: the compiler then no longer
+// waits for every outstanding global->LDS (buffer_load ... lds) transfer
+// before it, which it otherwise does because it cannot tell which LDS bytes
+// those transfers write. Callers order such transfers against the reads that
+// need them with an explicit s_waitcnt vmcnt(0) and a barrier.
+__device__ __forceinline__ bf16x4 lds_read_tr(const LDS_AS __bf16* __restrict__ p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4*)p);
 }
 typedef __fp16 fp16x4_builtin __attribute__((__vector_size__(4 * sizeof(__fp16))));
-__device__ __forceinline__ f16x4 lds_read_tr(const LDS_AS _Float16* p) {
+__device__ __forceinline__ f16x4 lds_read_tr(const LDS_AS _Float16* __restrict__ p) {
   return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS fp16x4_builtin*)p));
 }
 
