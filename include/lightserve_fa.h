@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define LSFA_ABI_VERSION 5
+#define LSFA_ABI_VERSION 6
 
 typedef enum {
   LSFA_DTYPE_FP32 = 0,
@@ -244,6 +244,54 @@ typedef struct {
   float eps;
 } lsfa_rmsnorm_args;
 
+/* Chunked prefill against a paged KV cache: a chunk of new query tokens per
+ * sequence attends to that sequence's cached keys (its earlier chunks and,
+ * written into the cache beforehand, the chunk itself). The reference's
+ * engine documents this as its missing prefill path (engine/request.py:86-93,
+ * engine/scheduler.py:34-44: num_scheduled_tokens > 1 has no kernel); the
+ * cache layout and block tables are its engine's (engine/config.py:5-7,
+ * engine/block_manager.py:56-60).
+ *   q          packed [total_q, heads_q, head_dim]; sequence b owns rows
+ *              cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1
+ *   k_cache,
+ *   v_cache    [num_blocks, block_size, heads_kv, head_dim]
+ *   block_tables int32 [batch, max_blocks_per_seq]
+ *   seq_lens_k int32 [batch]: cached keys of sequence b, the chunk included;
+ *              clamped on the device to max_blocks_per_seq * block_size
+ *   o          like q; lse fp32 [heads_q, total_q] (natural log) or NULL
+ * Causal masking is bottom-right aligned: query i of a chunk of n sits at
+ * position seq_lens_k[b] - n + i. Query head h reads KV head
+ * h / (heads_q / heads_kv). Block ids outside [0, num_blocks) read as zeros.
+ * block_size is a power of two and at least 16. */
+typedef struct {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  void* o;
+  float* lse;
+  const int32_t* cu_seqlens_q;
+  const int32_t* seq_lens_k;
+  const int32_t* block_tables;
+  int64_t q_stride[2];         /* token, head (head-dim stride 1) */
+  int64_t k_stride[3];         /* block, slot, head */
+  int64_t v_stride[3];
+  int64_t o_stride[2];
+  int64_t lse_stride[2];       /* head, token */
+  int64_t block_table_stride;
+  int32_t dtype;               /* bf16 or fp16 */
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t head_dim;            /* multiple of 8, at most 128 */
+  int32_t block_size;
+  int32_t num_blocks;
+  int32_t max_blocks_per_seq;
+  int32_t max_seqlen_q;        /* upper bound of the chunk lengths (sets the grid) */
+  int32_t causal;
+  float sm_scale;
+  int32_t reserved;
+} lsfa_prefill_paged_args;
+
 /* ABI version of the loaded library (LSFA_ABI_VERSION). */
 int lsfa_abi_version(void);
 
@@ -289,6 +337,14 @@ int lsfa_rope_check(const lsfa_rope_args* args);
 
 /* In-place RoPE of q and k (see lsfa_rope_args). */
 int lsfa_rope(const lsfa_rope_args* args, void* stream);
+
+/* Host-only validation of paged-prefill arguments; never touches the GPU. */
+int lsfa_prefill_paged_check(const lsfa_prefill_paged_args* args);
+
+/* Chunked prefill over a paged KV cache (see lsfa_prefill_paged_args): the
+ * forward kernel of lsfa_fwd with K/V tiles gathered through the block
+ * tables. No reference counterpart. */
+int lsfa_prefill_paged(const lsfa_prefill_paged_args* args, void* stream);
 
 /* Host-only validation of RMSNorm arguments; never touches the GPU. */
 int lsfa_rmsnorm_check(const lsfa_rmsnorm_args* args);

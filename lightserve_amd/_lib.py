@@ -13,7 +13,7 @@ import torch
 
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
 TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}
@@ -23,7 +23,8 @@ STATUS = {0: "LSFA_OK", -1: "LSFA_ERR_INVALID", -2: "LSFA_ERR_UNSUPPORTED", -3: 
 EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "lsfa_fwd",
                     "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd",
                     "lsfa_decode_check", "lsfa_decode_workspace_size", "lsfa_decode",
-                    "lsfa_rope_check", "lsfa_rope", "lsfa_rmsnorm_check", "lsfa_rmsnorm")
+                    "lsfa_rope_check", "lsfa_rope", "lsfa_rmsnorm_check", "lsfa_rmsnorm",
+                    "lsfa_prefill_paged_check", "lsfa_prefill_paged")
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -81,6 +82,22 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class PrefillPagedArgs(ctypes.Structure):
+    """Mirror of lsfa_prefill_paged_args."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("cu_seqlens_q", ctypes.c_void_p), ("seq_lens_k", ctypes.c_void_p), ("block_tables", ctypes.c_void_p),
+        ("q_stride", _i64x2), ("k_stride", _i64x3), ("v_stride", _i64x3), ("o_stride", _i64x2),
+        ("lse_stride", _i64x2), ("block_table_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("block_size", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32), ("max_blocks_per_seq", ctypes.c_int32),
+        ("max_seqlen_q", ctypes.c_int32), ("causal", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -131,12 +148,13 @@ def load():
         lib.lsfa_last_error.argtypes = []
         for name, struct in (("lsfa_fwd_check", FwdArgs), ("lsfa_bwd_check", BwdArgs),
                              ("lsfa_decode_check", DecodeArgs), ("lsfa_rope_check", RopeArgs),
-                             ("lsfa_rmsnorm_check", RmsNormArgs)):
+                             ("lsfa_rmsnorm_check", RmsNormArgs), ("lsfa_prefill_paged_check", PrefillPagedArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct)]
         for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_decode", DecodeArgs),
-                             ("lsfa_rope", RopeArgs), ("lsfa_rmsnorm", RmsNormArgs)):
+                             ("lsfa_rope", RopeArgs), ("lsfa_rmsnorm", RmsNormArgs),
+                             ("lsfa_prefill_paged", PrefillPagedArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
@@ -192,6 +210,16 @@ def decode_workspace_size(args):
 
 def decode(args, stream):
     _raise_on(load().lsfa_decode(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_decode")
+
+
+def prefill_paged_check(args):
+    """Host-only validation (no GPU access); returns (status, message)."""
+    rc = load().lsfa_prefill_paged_check(ctypes.byref(args))
+    return rc, load().lsfa_last_error().decode(errors="replace")
+
+
+def prefill_paged(args, stream):
+    _raise_on(load().lsfa_prefill_paged(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_prefill_paged")
 
 
 def rope_check(args):

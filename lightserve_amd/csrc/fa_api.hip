@@ -12,6 +12,7 @@
 
 namespace lsfa {
 hipError_t fwd_mfma(FwdParams p, bool is_bf16, int dp, bool causal, bool varlen, hipStream_t s);
+hipError_t fwd_paged(FwdParams p, bool is_bf16, int dp, bool causal, hipStream_t s);
 hipError_t bwd_mfma(const BwdParams& p, bool is_bf16, int dp, bool causal, hipStream_t s);
 hipError_t fwd_f32(const FwdParams& p, int dp, bool causal, bool varlen, float scale, hipStream_t s);
 hipError_t bwd_f32(const BwdParams& p, int dp, bool causal, hipStream_t s);
@@ -374,6 +375,75 @@ int lsfa_decode(const lsfa_decode_args* a, void* stream) {
   hipError_t e = lsfa::decode_gqa(p, a->dtype == LSFA_DTYPE_BF16, padded_decode_dim(a->head_dim),
                                   reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int lsfa_prefill_paged_check(const lsfa_prefill_paged_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  if (a->dtype != LSFA_DTYPE_FP16 && a->dtype != LSFA_DTYPE_BF16)
+    return fail(a->dtype == LSFA_DTYPE_FP32 ? LSFA_ERR_UNSUPPORTED : LSFA_ERR_INVALID,
+                "paged prefill supports bf16 and fp16 (dtype %d)", a->dtype);
+  if (a->batch < 0 || a->heads_q <= 0 || a->heads_kv <= 0 || a->num_blocks < 0 || a->max_blocks_per_seq < 0 ||
+      a->max_seqlen_q < 0)
+    return fail(LSFA_ERR_INVALID, "negative size or no heads (batch=%d heads_q=%d heads_kv=%d num_blocks=%d "
+                "max_blocks_per_seq=%d max_seqlen_q=%d)", a->batch, a->heads_q, a->heads_kv, a->num_blocks,
+                a->max_blocks_per_seq, a->max_seqlen_q);
+  if (a->heads_q % a->heads_kv != 0)
+    return fail(LSFA_ERR_INVALID, "heads_q (%d) is not a multiple of heads_kv (%d)", a->heads_q, a->heads_kv);
+  if (a->head_dim < 8 || a->head_dim > 128 || a->head_dim % 8 != 0)
+    return fail(LSFA_ERR_UNSUPPORTED, "paged prefill head_dim must be a multiple of 8 in 8..128 (got %d)", a->head_dim);
+  if (a->block_size < 16 || log2_exact(a->block_size) < 0)
+    return fail(LSFA_ERR_UNSUPPORTED, "paged prefill needs a power-of-two block_size of at least 16 (got %d)",
+                a->block_size);
+  if (!std::isfinite(a->sm_scale)) return fail(LSFA_ERR_INVALID, "sm_scale is not finite");
+  const long long tiles = (long long)((a->max_seqlen_q + 127) / 128) * a->batch * a->heads_q;
+  if (tiles > (1LL << 30)) return fail(LSFA_ERR_UNSUPPORTED, "problem too large for one launch");
+  if (a->batch == 0 || a->max_seqlen_q == 0) return ok();
+  if (!a->q || !a->k_cache || !a->v_cache || !a->o || !a->cu_seqlens_q || !a->seq_lens_k || !a->block_tables)
+    return fail(LSFA_ERR_INVALID, "q, k_cache, v_cache, o, cu_seqlens_q, seq_lens_k and block_tables must be non-NULL");
+  for (int i = 0; i < 2; ++i)
+    if (a->q_stride[i] % 8 != 0 || a->o_stride[i] % 8 != 0)
+      return fail(LSFA_ERR_UNSUPPORTED, "q/o strides must be multiples of 8 elements");
+  for (int i = 0; i < 3; ++i)
+    if (a->k_stride[i] % 8 != 0 || a->v_stride[i] % 8 != 0)
+      return fail(LSFA_ERR_UNSUPPORTED, "k_cache/v_cache strides must be multiples of 8 elements");
+  // 16 slots of one block are addressed from a per-wave base with 32-bit byte offsets.
+  if (a->k_stride[1] < 0 || a->k_stride[1] > (1LL << 22) || a->v_stride[1] < 0 || a->v_stride[1] > (1LL << 22))
+    return fail(LSFA_ERR_UNSUPPORTED, "cache slot strides must lie in 0..2^22 elements");
+  if (!aligned16(a->q) || !aligned16(a->o) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+    return fail(LSFA_ERR_UNSUPPORTED, "q, o, k_cache and v_cache must be 16-byte aligned");
+  if (a->block_table_stride < a->max_blocks_per_seq)
+    return fail(LSFA_ERR_INVALID, "block_table_stride %lld is below max_blocks_per_seq %d",
+                (long long)a->block_table_stride, a->max_blocks_per_seq);
+  return ok();
+}
+
+int lsfa_prefill_paged(const lsfa_prefill_paged_args* a, void* stream) {
+  int rc = lsfa_prefill_paged_check(a);
+  if (rc) return rc;
+  if (a->batch == 0 || a->max_seqlen_q == 0) return ok();
+  lsfa::FwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = a->q; p.k = a->k_cache; p.v = a->v_cache; p.o = a->o; p.lse = a->lse;
+  p.sqn = a->q_stride[0]; p.sqh = a->q_stride[1];
+  p.skb = a->k_stride[0]; p.skn = a->k_stride[1]; p.skh = a->k_stride[2];
+  p.svb = a->v_stride[0]; p.svn = a->v_stride[1]; p.svh = a->v_stride[2];
+  p.son = a->o_stride[0]; p.soh = a->o_stride[1];
+  p.slh = a->lse_stride[0]; p.sln = a->lse_stride[1];
+  p.cu_q = a->cu_seqlens_q;
+  p.block_tables = a->block_tables;
+  p.seq_lens_k = a->seq_lens_k;
+  p.sbt = a->block_table_stride;
+  p.block_shift = log2_exact(a->block_size);
+  p.max_blocks = a->max_blocks_per_seq;
+  p.num_blocks = a->num_blocks;
+  p.B = a->batch; p.Hq = a->heads_q; p.Hkv = a->heads_kv;
+  p.Nq = a->max_seqlen_q; p.Nk = 0; p.D = a->head_dim;
+  p.scale_log2 = fmaxf(fabsf(a->sm_scale) * 1.4426950408889634f, 1e-30f);
+  p.neg_q = a->sm_scale < 0.f;
+  hipError_t e = lsfa::fwd_paged(p, a->dtype == LSFA_DTYPE_BF16, padded_dim(a->head_dim), a->causal != 0,
+                                 reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "paged prefill launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

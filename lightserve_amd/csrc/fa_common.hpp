@@ -138,6 +138,14 @@ struct FwdParams {
   int64_t sqd, skd, svd, sod;  // head-dim strides (fp32 path only; 1 on the MFMA path)
   const int32_t* cu_q;
   const int32_t* cu_k;
+  // Paged K/V (chunked prefill against a KV cache): k/v are the caches
+  // [num_blocks, block_size, Hkv, D] with skb/svb the block stride, skn/svn
+  // the slot stride and skh/svh the head stride; keys per sequence come from
+  // seq_lens_k and their blocks from block_tables [B, max_blocks].
+  const int32_t* block_tables;
+  const int32_t* seq_lens_k;
+  int64_t sbt;  // block-table row stride
+  int block_shift, max_blocks, num_blocks;
   int B, Hq, Hkv, Nq, Nk, D;
   int num_q_tiles;
   float scale_log2;  // |sm_scale| * log2(e), at least 1e-30

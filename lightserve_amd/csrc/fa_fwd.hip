@@ -24,6 +24,14 @@
 //   every lane owns one query row: the row max/sum need one permlane32 swap.
 //   The fp32 S^T accumulator is rounded in registers into the B operand of
 //   O^T += V^T P^T; V^T comes from LDS through ds_read_b64_tr_b16.
+//
+// Paged K/V (PAGED, with packed varlen queries): the keys of sequence b are
+// its seq_lens_k[b] cache slots, found through its block-table row. A 64-key
+// tile is loaded as four 16-row pieces, one per wave; with block sizes that
+// are multiples of 16 each piece lies inside one cache block, so every wave
+// builds one buffer descriptor per tile from one block-table entry and the
+// LDS tile is the same as for contiguous K/V. Block ids outside
+// [0, num_blocks) read as zeros.
 #include "fa_common.hpp"
 
 namespace lsfa {
@@ -31,7 +39,7 @@ namespace lsfa {
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
-template <typename T, int DP, bool CAUSAL, bool VARLEN, bool LSE>
+template <typename T, int DP, bool CAUSAL, bool VARLEN, bool LSE, bool PAGED>
 __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
@@ -42,6 +50,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   constexpr int DT = DP / 32;
   constexpr int KB = BN / 32;
   static_assert(LDI >= 1, "tile too small for the workgroup");
+  static_assert(!PAGED || VARLEN, "paged K/V takes packed varlen queries");
+  static_assert(LDI * 1024 == 16 * DP * 2, "each wave loads 16 rows of a tile");
 
   __shared__ __attribute__((aligned(1024))) T smem_raw[4 * TILE];  // K0 K1 V0 V1
   LDS_AS T* smem = (LDS_AS T*)smem_raw;
@@ -59,16 +69,22 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   if (VARLEN) {
     rq0 = p.cu_q[b];
     nq = p.cu_q[b + 1] - (int)rq0;
-    rk0 = p.cu_k[b];
-    nk = p.cu_k[b + 1] - (int)rk0;
+    if (PAGED) {
+      nk = min(max(p.seq_lens_k[b], 0), p.max_blocks << p.block_shift);
+    } else {
+      rk0 = p.cu_k[b];
+      nk = p.cu_k[b + 1] - (int)rk0;
+    }
   }
   const int q0 = qt * BM;
   if (q0 >= nq) return;  // uniform across the workgroup, before any barrier
   const int off = nk - nq;  // bottom-right causal alignment
 
   const T* Q = (const T*)p.q + (VARLEN ? 0 : (int64_t)b * p.sqb) + (int64_t)h * p.sqh + rq0 * p.sqn;
-  const T* K = (const T*)p.k + (VARLEN ? 0 : (int64_t)b * p.skb) + (int64_t)hk * p.skh + rk0 * p.skn;
-  const T* V = (const T*)p.v + (VARLEN ? 0 : (int64_t)b * p.svb) + (int64_t)hk * p.svh + rk0 * p.svn;
+  const T* K = PAGED ? (const T*)p.k
+                     : (const T*)p.k + (VARLEN ? 0 : (int64_t)b * p.skb) + (int64_t)hk * p.skh + rk0 * p.skn;
+  const T* V = PAGED ? (const T*)p.v
+                     : (const T*)p.v + (VARLEN ? 0 : (int64_t)b * p.svb) + (int64_t)hk * p.svh + rk0 * p.svn;
   T* O = (T*)p.o + (VARLEN ? 0 : (int64_t)b * p.sob) + (int64_t)h * p.soh + rq0 * p.son;
 
   int kv_end = nk;
@@ -92,23 +108,37 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
     qreg[kk] = __builtin_bit_cast(X8, raw);
   }
 
-  // Direct global -> LDS tile load: wave w issues LDI 1 KB chunks; lane t of
-  // chunk c lands at tile byte (w*LDI + c)*1024 + 16t = (row, swizzled seg).
-  // The buffer descriptor is rebuilt per tile (scalar work) and clipped to
-  // the rows that exist, so the per-lane byte offsets are loop-invariant and
-  // rows at or past nk read as zero.
+  // Direct global -> LDS tile load: wave w issues LDI 1 KB chunks (tile rows
+  // 16w..16w+15); lane t of chunk c lands at tile byte (w*LDI + c)*1024 + 16t
+  // = (row, swizzled seg). The buffer descriptor is rebuilt per tile (scalar
+  // work) and clipped to the rows that exist, so the per-lane byte offsets
+  // are loop-invariant and rows at or past nk (and columns at or past D) read
+  // as zero. Paged offsets are relative to the wave's first row.
   int kvo[LDI], vvo[LDI];
 #pragma unroll
   for (int c = 0; c < LDI; ++c) {
     const int byte = (wave * LDI + c) * 1024 + lane * 16;
     const int row = byte / (DP * 2);
     const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
-    kvo[c] = (int)(row * p.skn * 2) + seg * 16;
-    vvo[c] = (int)(row * p.svn * 2) + seg * 16;
+    const int r = PAGED ? row - 16 * wave : row;
+    kvo[c] = seg * 8 < D ? (int)(r * p.skn * 2) + seg * 16 : (int)0x80000000;
+    vvo[c] = seg * 8 < D ? (int)(r * p.svn * 2) + seg * 16 : (int)0x80000000;
   }
-  auto tile_load = [&](const T* base, int64_t sn, const int* vo, int j, int buf) {
-    const int rows = min(nk - j * BN, BN);
-    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base + (int64_t)j * BN * sn, (int)(rows * sn * 2));
+  auto tile_load = [&](const T* base, int64_t sn, int64_t sblk, int64_t shead, const int* vo, int j, int buf) {
+    __amdgpu_buffer_rsrc_t rs;
+    if (PAGED) {
+      const int key0 = j * BN + 16 * wave;  // wave-uniform
+      const int rows = min(nk - key0, 16);
+      int blk = -1;
+      if (rows > 0) blk = __builtin_amdgcn_readfirstlane(p.block_tables[(int64_t)b * p.sbt + (key0 >> p.block_shift)]);
+      const bool live = rows > 0 && blk >= 0 && blk < p.num_blocks;
+      const int slot = key0 & ((1 << p.block_shift) - 1);
+      const T* src = live ? base + (int64_t)blk * sblk + (int64_t)slot * sn + (int64_t)hk * shead : base;
+      rs = tile_rsrc(src, live ? (int)(rows * sn * 2) : 0);
+    } else {
+      const int rows = min(nk - j * BN, BN);
+      rs = tile_rsrc(base + (int64_t)j * BN * sn, (int)(rows * sn * 2));
+    }
     LDS_AS char* dst = (LDS_AS char*)(smem + buf * TILE);
 #pragma unroll
     for (int c = 0; c < LDI; ++c)
@@ -224,9 +254,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   int n_full = min(ntiles, nk / BN);
   if (CAUSAL) n_full = min(n_full, max(0, q0 + off + 1) / BN);
 
-  tile_load(K, p.skn, kvo, 0, 0);
-  tile_load(V, p.svn, vvo, 0, 2);
-  tile_load(K, p.skn, kvo, 1, 1);  // past the end the descriptor is empty: zeros
+  tile_load(K, p.skn, p.skb, p.skh, kvo, 0, 0);
+  tile_load(V, p.svn, p.svb, p.svh, vvo, 0, 2);
+  tile_load(K, p.skn, p.skb, p.skh, kvo, 1, 1);  // past the end the descriptor is empty: zeros
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
@@ -239,8 +269,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   // One pipelined step: tile t's scores are in cur (offset already raised),
   // tile t+1's go to nxt.
   auto pipe_step = [&](int t, f32x16* cur, f32x16* nxt) {
-    tile_load(K, p.skn, kvo, t + 2, t & 1);
-    tile_load(V, p.svn, vvo, t + 1, 2 + ((t + 1) & 1));
+    tile_load(K, p.skn, p.skb, p.skh, kvo, t + 2, t & 1);
+    tile_load(V, p.svn, p.svb, p.svh, vvo, t + 1, 2 + ((t + 1) & 1));
     scores(kbuf(t + 1), nxt);
     X8 pb[2 * KB];
     softmax(cur, pb);
@@ -263,8 +293,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   // Remaining tiles (diagonal / sequence end), masked, one at a time. K of
   // tile n_full + 1 is already in flight from the pipelined part.
   for (; j < ntiles; ++j) {
-    if (j > n_full) tile_load(K, p.skn, kvo, j + 1, (j + 1) & 1);
-    tile_load(V, p.svn, vvo, j + 1, 2 + ((j + 1) & 1));
+    if (j > n_full) tile_load(K, p.skn, p.skb, p.skh, kvo, j + 1, (j + 1) & 1);
+    tile_load(V, p.svn, p.svb, p.svh, vvo, j + 1, 2 + ((j + 1) & 1));
     const int kbase = j * BN;
     const bool active = !CAUSAL || (kbase <= qw_lo + 31 + off);
     if (active) {
@@ -315,13 +345,13 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   }
 }
 
-template <typename T, int DP, bool CAUSAL, bool VARLEN>
+template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED = false>
 static hipError_t launch_fwd(const FwdParams& p, hipStream_t s) {
   const int total = p.num_q_tiles * p.B * p.Hq;
   if (p.lse != nullptr)
-    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, true>), dim3(total), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, true, PAGED>), dim3(total), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, false>), dim3(total), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, false, PAGED>), dim3(total), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
@@ -346,6 +376,28 @@ hipError_t fwd_mfma(FwdParams p, bool is_bf16, int dp, bool causal, bool varlen,
   p.num_q_tiles = (p.Nq + 127) / 128;
   if (is_bf16) return dispatch_fwd_t<__bf16>(p, dp, causal, varlen, s);
   return dispatch_fwd_t<_Float16>(p, dp, causal, varlen, s);
+}
+
+template <typename T, int DP>
+static hipError_t dispatch_paged_dp(const FwdParams& p, bool causal, hipStream_t s) {
+  return causal ? launch_fwd<T, DP, true, true, true>(p, s) : launch_fwd<T, DP, false, true, true>(p, s);
+}
+
+template <typename T>
+static hipError_t dispatch_paged_t(const FwdParams& p, int dp, bool causal, hipStream_t s) {
+  switch (dp) {
+    case 32: return dispatch_paged_dp<T, 32>(p, causal, s);
+    case 64: return dispatch_paged_dp<T, 64>(p, causal, s);
+    default: return dispatch_paged_dp<T, 128>(p, causal, s);
+  }
+}
+
+// Paged K/V forward (arguments validated by the C ABI layer; p.Nq is the
+// longest query chunk, block_shift >= 4).
+hipError_t fwd_paged(FwdParams p, bool is_bf16, int dp, bool causal, hipStream_t s) {
+  p.num_q_tiles = (p.Nq + 127) / 128;
+  if (is_bf16) return dispatch_paged_t<__bf16>(p, dp, causal, s);
+  return dispatch_paged_t<_Float16>(p, dp, causal, s);
 }
 
 }  // namespace lsfa

@@ -10,6 +10,7 @@ Contents
                 kernels/tests/test_flash_attention.py:47), its autograd
                 gradients, a line-by-line restatement of the reference's
                 tiled forward/backward loops, varlen/GQA, paged-KV decode,
+                paged-KV chunked prefill,
                 and a pure-Python loop version for tiny inputs.
   inputs.py     the seeded input recipe of the five BASELINE configurations.
   model.py      the reference's model forward in plain torch (RoPE tables and
@@ -26,6 +27,10 @@ How each function is pinned (tests/test_oracle.py):
   paged_decode_reference  pure-Python loops over a hand-built cache, the
                         dense closed form through an identity block table,
                         and invariance under a permutation of the blocks.
+  paged_prefill_reference  pure-Python loops (ragged chunks, GQA, empty
+                        chunks), a block permutation, and the chunking
+                        invariant (chunk-by-chunk prefill equals one causal
+                        pass); a planted top-left mask fails it.
   model.apply_rope      RoPE as an element-by-element rotation (tests/test_oracle_model.py).
   model.add_rmsnorm_reference  h and out written out by hand per element
                         (pure-Python sums), with and without the residual; unit

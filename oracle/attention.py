@@ -212,3 +212,37 @@ def paged_decode_reference(q, k_cache, v_cache, block_tables, seq_lens, sm_scale
         outs.append(o[:, 0])
         lses.append(lse[:, 0])
     return torch.stack(outs), torch.stack(lses)
+
+
+def gather_paged(cache, block_table_row, n):
+    """The first n token rows [n, Hkv, D] of one sequence in a paged cache
+    [num_blocks, block_size, Hkv, D]: entry i of its block-table row holds
+    tokens [i*block_size, (i+1)*block_size) (engine/block_manager.py:56-60)."""
+    bs = cache.shape[1]
+    nblk = (n + bs - 1) // bs
+    ids = block_table_row[:nblk].long().cpu()
+    return cache.cpu()[ids].reshape(nblk * bs, *cache.shape[2:])[:n]
+
+
+def paged_prefill_reference(q, k_cache, v_cache, block_tables, cu_seqlens_q, seq_lens_k, causal=True,
+                            sm_scale=None, *, dtype=torch.float64):
+    """Chunked prefill over a paged KV cache: sequence b's chunk
+    q[cu_seqlens_q[b]:cu_seqlens_q[b+1]] attends to its seq_lens_k[b] cached
+    keys (gathered with gather_paged), bottom-right causal, KV heads expanded
+    h -> h // group. q [Tq, Hq, D]; returns (o [Tq, Hq, D], lse [Hq, Tq]) in
+    `dtype`; a query that sees no key gives o = 0, lse = -inf."""
+    Tq, Hq, D = q.shape
+    group = Hq // k_cache.shape[2]
+    cq = [int(x) for x in cu_seqlens_q]
+    o = torch.zeros((Tq, Hq, D), dtype=dtype)
+    lse = torch.full((Hq, Tq), float("-inf"), dtype=dtype)
+    for b in range(len(cq) - 1):
+        nq, nk = cq[b + 1] - cq[b], int(seq_lens_k[b])
+        if nq == 0 or nk == 0:
+            continue
+        kb = gather_paged(k_cache, block_tables[b], nk).transpose(0, 1).repeat_interleave(group, 0)
+        vb = gather_paged(v_cache, block_tables[b], nk).transpose(0, 1).repeat_interleave(group, 0)
+        ob, lb = attention_reference(q[cq[b]:cq[b + 1]].cpu().transpose(0, 1), kb, vb, causal, sm_scale, dtype=dtype)
+        o[cq[b]:cq[b + 1]] = ob.transpose(0, 1)
+        lse[:, cq[b]:cq[b + 1]] = lb
+    return o, lse

@@ -111,7 +111,10 @@ def test_struct_layout_matches_header(built_library):
            ' sizeof(lsfa_decode_args), offsetof(lsfa_decode_args, block_table_stride),'
            ' offsetof(lsfa_decode_args, sm_scale), sizeof(lsfa_rope_args), offsetof(lsfa_rope_args, table_stride),'
            ' offsetof(lsfa_rope_args, max_pos)); printf("%zu %zu %zu\\n", sizeof(lsfa_rmsnorm_args),'
-           ' offsetof(lsfa_rmsnorm_args, dtype), offsetof(lsfa_rmsnorm_args, eps)); return 0;}\n')
+           ' offsetof(lsfa_rmsnorm_args, dtype), offsetof(lsfa_rmsnorm_args, eps));'
+           ' printf("%zu %zu %zu %zu\\n", sizeof(lsfa_prefill_paged_args),'
+           ' offsetof(lsfa_prefill_paged_args, block_table_stride), offsetof(lsfa_prefill_paged_args, causal),'
+           ' offsetof(lsfa_prefill_paged_args, sm_scale)); return 0;}\n')
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "t.c")
         exe = os.path.join(d, "t")
@@ -122,7 +125,9 @@ def test_struct_layout_matches_header(built_library):
                      _lib.FwdArgs.sm_scale.offset, _lib.BwdArgs.sm_scale.offset, ctypes.sizeof(_lib.DecodeArgs),
                      _lib.DecodeArgs.block_table_stride.offset, _lib.DecodeArgs.sm_scale.offset,
                      ctypes.sizeof(_lib.RopeArgs), _lib.RopeArgs.table_stride.offset, _lib.RopeArgs.max_pos.offset,
-                     ctypes.sizeof(_lib.RmsNormArgs), _lib.RmsNormArgs.dtype.offset, _lib.RmsNormArgs.eps.offset]
+                     ctypes.sizeof(_lib.RmsNormArgs), _lib.RmsNormArgs.dtype.offset, _lib.RmsNormArgs.eps.offset,
+                     ctypes.sizeof(_lib.PrefillPagedArgs), _lib.PrefillPagedArgs.block_table_stride.offset,
+                     _lib.PrefillPagedArgs.causal.offset, _lib.PrefillPagedArgs.sm_scale.offset]
 
 
 def _fwd_args(**kw):
@@ -258,6 +263,45 @@ def test_abi_rope_validation(built_library):
     _lib.rope(_rope_args(seqlen=0, q=None, k=None), 0)
     with pytest.raises(RuntimeError, match="LSFA_ERR_INVALID"):
         _lib.rope(_rope_args(batch=-1), 0)
+
+
+def _prefill_args(**kw):
+    base = dict(q=4096, k_cache=8192, v_cache=12288, o=16384, lse=None, cu_seqlens_q=20480, seq_lens_k=24576,
+                block_tables=28672, q_stride=_lib._i64x2(1024, 128), k_stride=_lib._i64x3(16 * 2 * 128, 256, 128),
+                v_stride=_lib._i64x3(16 * 2 * 128, 256, 128), o_stride=_lib._i64x2(1024, 128),
+                lse_stride=_lib._i64x2(64, 1), block_table_stride=8, dtype=_lib.DTYPE_BF16, batch=2, heads_q=8,
+                heads_kv=2, head_dim=128, block_size=16, num_blocks=16, max_blocks_per_seq=8, max_seqlen_q=32,
+                causal=1, sm_scale=0.088, reserved=0)
+    base.update(kw)
+    return _lib.PrefillPagedArgs(**base)
+
+
+def test_abi_prefill_paged_validation(built_library):
+    """Host-only validation of lsfa_prefill_paged (fake, never dereferenced pointers)."""
+    assert _lib.prefill_paged_check(_prefill_args())[0] == 0
+    assert _lib.prefill_paged_check(_prefill_args(heads_q=6))[0] == 0  # group of 3 is fine here
+    assert _lib.prefill_paged_check(_prefill_args(batch=0, q=None))[0] == 0  # empty: nothing checked further
+    rc, msg = _lib.prefill_paged_check(_prefill_args(block_size=8))
+    assert rc == -2 and "block_size" in msg
+    rc, msg = _lib.prefill_paged_check(_prefill_args(block_size=48))
+    assert rc == -2
+    rc, msg = _lib.prefill_paged_check(_prefill_args(dtype=_lib.DTYPE_FP32))
+    assert rc == -2
+    rc, msg = _lib.prefill_paged_check(_prefill_args(heads_q=5))
+    assert rc == -1 and "multiple" in msg
+    rc, msg = _lib.prefill_paged_check(_prefill_args(head_dim=100))
+    assert rc == -2
+    rc, msg = _lib.prefill_paged_check(_prefill_args(block_tables=None))
+    assert rc == -1
+    rc, msg = _lib.prefill_paged_check(_prefill_args(block_table_stride=4))
+    assert rc == -1 and "block_table_stride" in msg
+    rc, msg = _lib.prefill_paged_check(_prefill_args(q=4100))
+    assert rc == -2 and "aligned" in msg
+    rc, msg = _lib.prefill_paged_check(_prefill_args(sm_scale=float("inf")))
+    assert rc == -1
+    _lib.prefill_paged(_prefill_args(batch=0), 0)  # empty: no-op, no GPU touched
+    with pytest.raises(RuntimeError, match="block_size"):
+        _lib.prefill_paged(_prefill_args(block_size=4), 0)
 
 
 def _norm_args(**kw):

@@ -10,6 +10,10 @@ Checks, per oracle function:
   varlen_reference     vs pure-Python loops with GQA;
   paged_decode_reference vs pure-Python loops on a cache the test scatters
                        itself, and invariance under a block permutation;
+  paged_prefill_reference vs pure-Python loops (ragged chunks, GQA, empty
+                       chunks and sequences), a block permutation, and the
+                       chunking invariant: prefilling a sequence chunk by
+                       chunk gives the rows of one causal pass over all of it;
 and planted mistakes in copies of the oracle must fail these checks.
 """
 import math
@@ -22,7 +26,7 @@ import torch.nn.functional as F
 
 from oracle.attention import (attention_grads, attention_reference, bwd_delta, causal_mask,
                               flash_backward_tiled, flash_forward_tiled, naive_attention,
-                              paged_decode_reference, varlen_reference)
+                              gather_paged, paged_decode_reference, paged_prefill_reference, varlen_reference)
 from oracle.inputs import CONFIGS, make_config_inputs, make_varlen_inputs, varlen_fwd_flops
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "attention_golden.npz")
@@ -293,3 +297,83 @@ def test_planted_mistakes_are_caught(golden, broken):
         if not np.allclose(o.numpy(), golden[f"{name}/o"], atol=1e-9):
             caught += 1
     assert caught > 0, f"{broken.__name__} passed every golden case"
+
+
+def _prefill_case(seed, lens_k, lens_q, hq, hkv, d, bs, num_blocks, perm):
+    g = torch.Generator().manual_seed(seed)
+    seqs_k = [torch.randn(n, hkv, d, generator=g, dtype=torch.float64) for n in lens_k]
+    seqs_v = [torch.randn(n, hkv, d, generator=g, dtype=torch.float64) for n in lens_k]
+    q = torch.randn(sum(lens_q), hq, d, generator=g, dtype=torch.float64)
+    cu = torch.tensor([0] + list(np.cumsum(lens_q)), dtype=torch.int32)
+    kc, vc, table = _scatter_cache(seqs_k, seqs_v, bs, num_blocks, perm)
+    return q, cu, seqs_k, seqs_v, kc, vc, table
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_paged_prefill_matches_loops(causal):
+    lens_k, lens_q, hq, hkv, d, bs = [9, 5, 0, 12, 3], [4, 5, 0, 1, 0], 4, 2, 4, 4
+    q, cu, seqs_k, seqs_v, kc, vc, table = _prefill_case(21, lens_k, lens_q, hq, hkv, d, bs, 12,
+                                                         [5, 0, 11, 2, 7, 9, 1, 3, 10, 4, 6, 8])
+    sl = torch.tensor(lens_k, dtype=torch.int32)
+    o, lse = paged_prefill_reference(q, kc, vc, table, cu, sl, causal, 0.4)
+    for b in range(len(lens_k)):
+        rows = slice(int(cu[b]), int(cu[b + 1]))
+        if lens_q[b] == 0:
+            continue
+        if lens_k[b] == 0:
+            assert torch.equal(o[rows], torch.zeros_like(o[rows])) and torch.isinf(lse[:, rows]).all()
+            continue
+        on, ln = naive_attention(q[rows].transpose(0, 1).tolist(), seqs_k[b].transpose(0, 1).tolist(),
+                                 seqs_v[b].transpose(0, 1).tolist(), causal, 0.4, group=hq // hkv)
+        np.testing.assert_allclose(o[rows].transpose(0, 1).numpy(), np.array(on), atol=1e-12)
+        np.testing.assert_allclose(lse[:, rows].numpy(), np.array(ln), atol=1e-12)
+
+
+def test_paged_prefill_block_permutation():
+    args = ([10, 7], [3, 7], 2, 1, 8, 4, 6)
+    a = _prefill_case(22, *args, list(range(6)))
+    b = _prefill_case(22, *args, [4, 2, 5, 0, 3, 1])
+    sl = torch.tensor(args[0], dtype=torch.int32)
+    ra = paged_prefill_reference(a[0], a[4], a[5], a[6], a[1], sl)
+    rb = paged_prefill_reference(b[0], b[4], b[5], b[6], b[1], sl)
+    torch.testing.assert_close(ra[0], rb[0], atol=1e-14, rtol=0)
+    torch.testing.assert_close(ra[1], rb[1], atol=1e-14, rtol=0)
+
+
+def _chunked_prefill(oracle_fn, q_full, kc, vc, table, chunks):
+    """Runs a sequence's prefill chunk by chunk: chunk c attends to the keys
+    cached so far (its own included). Returns the concatenated outputs."""
+    outs, start = [], 0
+    for c in chunks:
+        cu = torch.tensor([0, c], dtype=torch.int32)
+        o, _ = oracle_fn(q_full[start:start + c], kc, vc, table, cu, torch.tensor([start + c], dtype=torch.int32))
+        outs.append(o)
+        start += c
+    return torch.cat(outs)
+
+
+def test_paged_prefill_chunking_invariant():
+    n, hq, hkv, d, bs = 13, 4, 2, 8, 4
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn(n, hq, d, generator=g, dtype=torch.float64)
+    k = torch.randn(n, hkv, d, generator=g, dtype=torch.float64)
+    v = torch.randn(n, hkv, d, generator=g, dtype=torch.float64)
+    kc, vc, table = _scatter_cache([k], [v], bs, 4, [2, 0, 3, 1])
+    whole, _ = varlen_reference(q, k, v, torch.tensor([0, n]), torch.tensor([0, n]), causal=True)
+    for chunks in ([13], [5, 8], [4, 4, 4, 1], [1] * 13):
+        torch.testing.assert_close(_chunked_prefill(paged_prefill_reference, q, kc, vc, table, chunks), whole,
+                                   atol=1e-12, rtol=0)
+
+    # planted mistake: top-left causal alignment (query i of a chunk sees keys
+    # 0..i, as SDPA's is_causal does for Nq != Nk) breaks the invariant
+    def top_left(qc, kc_, vc_, table_, cu, sl):
+        nq, nk = qc.shape[0], int(sl[0])
+        kk = gather_paged(kc_, table_[0], nk).transpose(0, 1)
+        vv = gather_paged(vc_, table_[0], nk).transpose(0, 1)
+        kk, vv = kk.repeat_interleave(hq // hkv, 0), vv.repeat_interleave(hq // hkv, 0)
+        s = torch.matmul(qc.transpose(0, 1), kk.transpose(-1, -2)) / math.sqrt(d)
+        mask = torch.arange(nk).view(1, -1) <= torch.arange(nq).view(-1, 1)
+        p = torch.softmax(s.masked_fill(~mask, float("-inf")), -1)
+        return torch.matmul(p, vv).transpose(0, 1), None
+    bad = _chunked_prefill(top_left, q, kc, vc, table, [5, 8])
+    assert (bad - whole).abs().max() > 1e-3
