@@ -124,13 +124,25 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
     kvo[c] = seg * 8 < D ? (int)(r * p.skn * 2) + seg * 16 : (int)0x80000000;
     vvo[c] = seg * 8 < D ? (int)(r * p.svn * 2) + seg * 16 : (int)0x80000000;
   }
-  auto tile_load = [&](const T* base, int64_t sn, int64_t sblk, int64_t shead, const int* vo, int j, int buf) {
+  // Paged: the cache block holding this wave's 16 rows of tile j (-1 past
+  // the sequence). The table is read through the constant address space (it
+  // does not change during a launch), so the wave-uniform read is one scalar
+  // load into an SGPR, issued one pipelined iteration before the tile load
+  // that uses it; it completes under the previous iteration's closing waits.
+  auto block_of = [&](int j) -> int {
+    if (!PAGED) return 0;
+    const int key0 = j * BN + 16 * wave;  // wave-uniform
+    if (key0 >= nk) return -1;
+    const __attribute__((address_space(4))) int32_t* bt = (const __attribute__((address_space(4))) int32_t*)p.block_tables;
+    return bt[(int64_t)b * p.sbt + (key0 >> p.block_shift)];
+  };
+  auto tile_load = [&](const T* base, int64_t sn, int64_t sblk, int64_t shead, const int* vo, int j, int buf,
+                       int blk) {
     __amdgpu_buffer_rsrc_t rs;
     if (PAGED) {
       const int key0 = j * BN + 16 * wave;  // wave-uniform
       const int rows = min(nk - key0, 16);
-      int blk = -1;
-      if (rows > 0) blk = __builtin_amdgcn_readfirstlane(p.block_tables[(int64_t)b * p.sbt + (key0 >> p.block_shift)]);
+      blk = __builtin_amdgcn_readfirstlane(blk);
       const bool live = rows > 0 && blk >= 0 && blk < p.num_blocks;
       const int slot = key0 & ((1 << p.block_shift) - 1);
       const T* src = live ? base + (int64_t)blk * sblk + (int64_t)slot * sn + (int64_t)hk * shead : base;
@@ -254,9 +266,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   int n_full = min(ntiles, nk / BN);
   if (CAUSAL) n_full = min(n_full, max(0, q0 + off + 1) / BN);
 
-  tile_load(K, p.skn, p.skb, p.skh, kvo, 0, 0);
-  tile_load(V, p.svn, p.svb, p.svh, vvo, 0, 2);
-  tile_load(K, p.skn, p.skb, p.skh, kvo, 1, 1);  // past the end the descriptor is empty: zeros
+  // blk1, blk2: blocks of tiles t+1 and t+2 for the next pipelined step t.
+  const int blk0 = block_of(0);
+  int blk1 = block_of(1), blk2 = block_of(2);
+  tile_load(K, p.skn, p.skb, p.skh, kvo, 0, 0, blk0);
+  tile_load(V, p.svn, p.svb, p.svh, vvo, 0, 2, blk0);
+  tile_load(K, p.skn, p.skb, p.skh, kvo, 1, 1, blk1);  // past the end the descriptor is empty: zeros
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
@@ -269,8 +284,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   // One pipelined step: tile t's scores are in cur (offset already raised),
   // tile t+1's go to nxt.
   auto pipe_step = [&](int t, f32x16* cur, f32x16* nxt) {
-    tile_load(K, p.skn, p.skb, p.skh, kvo, t + 2, t & 1);
-    tile_load(V, p.svn, p.svb, p.svh, vvo, t + 1, 2 + ((t + 1) & 1));
+    tile_load(K, p.skn, p.skb, p.skh, kvo, t + 2, t & 1, blk2);
+    tile_load(V, p.svn, p.svb, p.svh, vvo, t + 1, 2 + ((t + 1) & 1), blk1);
     scores(kbuf(t + 1), nxt);
     X8 pb[2 * KB];
     softmax(cur, pb);
@@ -278,6 +293,13 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
     const float mxs = row_max(nxt);
     if (t + 1 < n_full) raise_offset(mxs);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (PAGED) {
+      // The next step's block id is read after this step's last LDS read:
+      // an outstanding scalar load holds up every LDS wait issued after it,
+      // so here its latency only overlaps the barrier's own wait.
+      blk1 = blk2;
+      blk2 = block_of(t + 3);
+    }
     __syncthreads();
   };
   int j = 0;
@@ -293,8 +315,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   // Remaining tiles (diagonal / sequence end), masked, one at a time. K of
   // tile n_full + 1 is already in flight from the pipelined part.
   for (; j < ntiles; ++j) {
-    if (j > n_full) tile_load(K, p.skn, p.skb, p.skh, kvo, j + 1, (j + 1) & 1);
-    tile_load(V, p.svn, p.svb, p.svh, vvo, j + 1, 2 + ((j + 1) & 1));
+    const int bj = block_of(j + 1);
+    if (j > n_full) tile_load(K, p.skn, p.skb, p.skh, kvo, j + 1, (j + 1) & 1, bj);
+    tile_load(V, p.svn, p.svb, p.svh, vvo, j + 1, 2 + ((j + 1) & 1), bj);
     const int kbase = j * BN;
     const bool active = !CAUSAL || (kbase <= qw_lo + 31 + off);
     if (active) {

@@ -1,11 +1,12 @@
-"""Seeded inputs of the five BASELINE configurations -- test infrastructure only.
+"""Seeded synthetic inputs and FLOP counts of the five benchmark workloads.
 
-Recipe (fixed here; BASELINE names only shapes, scales and seeds): a CPU
-torch.Generator seeded with the config's seed draws fp32 randn tensors in the
-order q, k, v, (dO), then config-specific extras; the scale factor is
-applied in fp32, then the tensors are cast to the config dtype. Oracles use
+Recipe (fixed here; the workload definitions name only shapes, scales and
+seeds): a CPU torch.Generator seeded with the config's seed draws fp32 randn
+tensors in the order q, k, v, (dO), then config-specific extras; the scale
+factor is applied in fp32, then the tensors are cast to the config dtype. Oracles use
 the cast values upcast to fp32/fp64. bench.py and the GPU tests both build
-their inputs from here, so they see identical data.
+their inputs from here, so they see identical data. Nothing on the kernel
+path imports this module.
 """
 import torch
 

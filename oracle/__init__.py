@@ -12,7 +12,6 @@ Contents
                 tiled forward/backward loops, varlen/GQA, paged-KV decode,
                 paged-KV chunked prefill,
                 and a pure-Python loop version for tiny inputs.
-  inputs.py     the seeded input recipe of the five BASELINE configurations.
   model.py      the reference's model forward in plain torch (RoPE tables and
                 rotation, RMSNorm, the fused add + RMSNorm's semantics,
                 reference_llama_forward, with GQA).

@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
 from oracle.attention import naive_attention  # noqa: E402
-from oracle.inputs import make_config_inputs  # noqa: E402
+from lightserve_amd.workloads import make_config_inputs  # noqa: E402
 
 
 def tensor_sha256(t):

@@ -14,7 +14,7 @@ from lightserve_amd.kernels.flash_attention import flash_attention_forward
 from lightserve_amd.kernels.flash_attention_backward import (_flash_attention_backward, _flash_attention_forward_lse,
                                                              flash_attention)
 from oracle.attention import attention_grads, attention_reference, flash_backward_tiled
-from oracle.inputs import make_config_inputs
+from lightserve_amd.workloads import make_config_inputs
 from tests.gates import assert_gate, assert_grad_parity
 
 pytestmark = pytest.mark.gpu

@@ -15,7 +15,7 @@ import torch
 
 from lightserve_amd.kernels.flash_attention import flash_attention_forward
 from oracle.attention import attention_reference
-from oracle.inputs import make_config_inputs
+from lightserve_amd.workloads import make_config_inputs
 from tests.gates import assert_gate, assert_lse
 
 pytestmark = pytest.mark.gpu

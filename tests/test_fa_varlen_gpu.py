@@ -5,7 +5,7 @@ import torch
 
 from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen_forward
 from oracle.attention import attention_reference, varlen_reference
-from oracle.inputs import make_varlen_inputs
+from lightserve_amd.workloads import make_varlen_inputs
 from tests.gates import assert_gate, assert_lse
 
 pytestmark = pytest.mark.gpu

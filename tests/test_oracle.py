@@ -27,7 +27,7 @@ import torch.nn.functional as F
 from oracle.attention import (attention_grads, attention_reference, bwd_delta, causal_mask,
                               flash_backward_tiled, flash_forward_tiled, naive_attention,
                               gather_paged, paged_decode_reference, paged_prefill_reference, varlen_reference)
-from oracle.inputs import CONFIGS, make_config_inputs, make_varlen_inputs, varlen_fwd_flops
+from lightserve_amd.workloads import CONFIGS, make_config_inputs, make_varlen_inputs, varlen_fwd_flops
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "attention_golden.npz")
 
