@@ -29,7 +29,7 @@ import statistics
 import torch
 import torch.nn.functional as F
 
-from ..kernels.paged_attention import paged_attention_decode
+from ..kernels.paged_attention import paged_attention_decode, paged_prefill
 from ..kernels.rope import apply_rope_
 from ..kernels.fused_rmsnorm_residual import fused_add_rmsnorm
 from .minimal_llama import add_norm, init_weights, llama3_8b_shape, llama_forward, precompute_rope
@@ -113,7 +113,8 @@ class KVCacheDecoder:
 
     State on the device: tokens [B] (the step's input), seq_lens [B] (tokens
     cached so far), k/v caches per layer and the block tables. step() issues
-    only device work of static shape, so it can be captured and replayed."""
+    only device work of static shape, so it can be captured and replayed;
+    prefill() caches a prompt chunk by chunk before the decode steps."""
 
     def __init__(self, weights, config, batch_size, block_size=16, device="cuda", shuffle_blocks=True, seed=0):
         self.w, self.cfg, self.B = weights, config, batch_size
@@ -157,6 +158,50 @@ class KVCacheDecoder:
             pending = torch.matmul(mlp, layer.down_proj)
         final, _ = add_norm(pending, residual, self.w.norm_weight, cfg.rms_eps)
         return torch.matmul(final, self.w.lm_head)
+
+    def prefill(self, prompt, chunk_size):
+        """Caches a prompt [B, P] chunk by chunk (the engine's chunked prefill:
+        each chunk's K/V rows are rotated at their positions and written into
+        the paged cache, then the chunk's queries attend to everything cached
+        so far through paged_prefill). Returns the logits [B, vocab] of the
+        last prompt token and makes their argmax the next decode token."""
+        cfg, B = self.cfg, self.B
+        nh, nkv, hd, H = cfg.n_heads, cfg.kv_heads, cfg.head_dim, cfg.hidden_size
+        assert prompt.shape[0] == B and prompt.shape[1] > 0, "prompt must be [batch, P] with P > 0"
+        P = prompt.shape[1]
+        logits = None
+        for s in range(0, P, chunk_size):
+            c = min(chunk_size, P - s)
+            pos = self.seq_lens  # [B] first position of the chunk
+            t = torch.arange(c, device=pos.device, dtype=torch.int32)
+            abs_pos = (pos.view(B, 1) + t.view(1, c)).long()  # [B, c]
+            slot = (self.block_tables.gather(1, abs_pos // self.bs).long() * self.bs + abs_pos % self.bs).view(-1)
+            cu = torch.arange(0, (B + 1) * c, c, device=pos.device, dtype=torch.int32)
+            lens = pos + c
+            residual = F.embedding(prompt[:, s:s + c].reshape(-1), self.w.embed_tokens)  # [B*c, H]
+            pending = None
+            for i, layer in enumerate(self.w.layers):
+                h, residual = add_norm(pending, residual, layer.input_layernorm_weight, cfg.rms_eps)
+                q = torch.matmul(h, layer.q_proj)
+                k = torch.matmul(h, layer.k_proj)
+                v = torch.matmul(h, layer.v_proj)
+                apply_rope_(q.view(B, c, nh, hd).transpose(1, 2), k.view(B, c, nkv, hd).transpose(1, 2),
+                            self.cos, self.sin, positions=pos)
+                self.k_cache[i].view(-1, nkv, hd).index_copy_(0, slot, k.view(B * c, nkv, hd))
+                self.v_cache[i].view(-1, nkv, hd).index_copy_(0, slot, v.view(B * c, nkv, hd))
+                o = paged_prefill(q.view(B * c, nh, hd), self.k_cache[i], self.v_cache[i], self.block_tables, cu, lens,
+                                  max_seqlen_q=c)
+                h2, residual = fused_add_rmsnorm(torch.matmul(o.view(B * c, nh * hd), layer.o_proj), residual,
+                                                 layer.post_attention_layernorm_weight, cfg.rms_eps)
+                mlp = F.silu(torch.matmul(h2, layer.gate_proj)) * torch.matmul(h2, layer.up_proj)
+                pending = torch.matmul(mlp, layer.down_proj)
+            last = slice(c - 1, B * c, c)  # each sequence's last token of the chunk
+            final, _ = add_norm(pending[last].contiguous() if pending is not None else None,
+                                residual[last].contiguous(), self.w.norm_weight, cfg.rms_eps)
+            logits = torch.matmul(final, self.w.lm_head)
+            self.seq_lens.add_(c)
+        self.tokens.copy_(logits.argmax(dim=-1))
+        return logits
 
     def advance(self, logits):
         """Greedy next token; one more cached token per sequence."""
@@ -211,6 +256,38 @@ def reset(dec, config, args):
     return dec
 
 
+def prefill_main(args):
+    """Times KVCacheDecoder.prefill of a P-token prompt per sequence (chunks
+    of --chunk tokens; HIP events around each whole prefill, median of
+    --num-steps runs after --warmup-steps, each from an empty cache)."""
+    P, C = args.prefill, args.chunk
+    config = llama3_8b_shape(n_layers=args.n_layers, max_seq_len=max(args.max_seq_len, P + 1), gqa=args.gqa)
+    weights = init_weights(config, device="cuda", seed=args.seed)
+    prompt = torch.randint(0, config.vocab_size, (args.batch_size, P), generator=torch.Generator().manual_seed(1))
+    prompt = prompt.cuda()
+    dec = KVCacheDecoder(weights, config, args.batch_size, block_size=args.block_size)
+    lat = []
+    for i in range(args.warmup_steps + args.num_steps):
+        dec.seq_lens.zero_()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dec.prefill(prompt, C)
+        e1.record()
+        torch.cuda.synchronize()
+        if i >= args.warmup_steps:
+            lat.append(e0.elapsed_time(e1))
+    med = statistics.median(lat)
+    tokens = args.batch_size * P
+    res = {"prefill_tokens": P, "chunk": C, "batch_size": args.batch_size, "n_layers": config.n_layers,
+           "n_kv_heads": config.kv_heads, "median_ms": med, "tokens_per_s": tokens / (med * 1e-3)}
+    print(json.dumps(res), flush=True)
+    if args.out:
+        with open(args.out, "w") as f:
+            json.dump(res, f, indent=2)
+    return res
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--mode", choices=["full", "kvcache", "both"], default="both")
@@ -223,8 +300,14 @@ def main(argv=None):
     ap.add_argument("--gqa", action="store_true", help="LLaMA-3-8B's real 8 KV heads (kvcache mode and full)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--out", default=None, help="write the results JSON here")
+    ap.add_argument("--prefill", type=int, default=0, metavar="P",
+                    help="instead of decode steps: time the chunked prefill of a P-token prompt per sequence "
+                         "(max_seq_len is raised to fit it)")
+    ap.add_argument("--chunk", type=int, default=512, help="prefill chunk size")
     args = ap.parse_args(argv)
     assert torch.cuda.is_available(), "needs a GPU"
+    if args.prefill:
+        return prefill_main(args)
     config = llama3_8b_shape(n_layers=args.n_layers, max_seq_len=args.max_seq_len, gqa=args.gqa)
     needed = args.warmup_steps + args.num_steps + 3
     assert needed < config.max_seq_len, f"--max-seq-len {config.max_seq_len} too small for {needed} decode steps"

@@ -173,6 +173,31 @@ def test_kvcache_decode_matches_full_forward(n_kv_heads, block_size):
         ids = torch.cat([ids, dec.tokens.view(2, 1)], dim=1)
 
 
+@pytest.mark.parametrize("n_kv_heads,chunk", [(2, 7), (None, 16), (1, 1)])
+def test_chunked_prefill_then_decode_matches_full_forward(n_kv_heads, chunk):
+    """A prompt cached chunk by chunk through paged_prefill (RoPE at each
+    chunk's positions, K/V written into a shuffled paged cache of 16-token
+    blocks) gives the full forward's logits for the prompt's last token, and
+    the decode steps after it continue to match the full forward."""
+    from lightserve_amd.model.graph_decode import KVCacheDecoder
+    print(f"case chunked prefill kv={n_kv_heads} chunk={chunk}", flush=True)
+    config = replace(TOY_CONFIG, n_kv_heads=n_kv_heads)
+    weights = init_weights(config, device="cuda", seed=0)
+    dec = KVCacheDecoder(weights, config, batch_size=2, block_size=16)
+    prompt = torch.randint(0, config.vocab_size, (2, 20), generator=torch.Generator().manual_seed(3)).cuda()
+    logits = dec.prefill(prompt, chunk)
+    full = llama_forward(weights, config, prompt)[:, -1]
+    torch.testing.assert_close(logits.float(), full.float(), atol=8e-2, rtol=8e-2, msg="prefill")
+    assert torch.equal(dec.seq_lens.cpu(), torch.tensor([20, 20], dtype=torch.int32))
+    ids = torch.cat([prompt, dec.tokens.view(2, 1)], dim=1)
+    for t in range(4):
+        logits = dec.step()
+        full = llama_forward(weights, config, ids)[:, -1]
+        torch.testing.assert_close(logits.float(), full.float(), atol=8e-2, rtol=8e-2, msg=f"decode step {t}")
+        dec.advance(logits)
+        ids = torch.cat([ids, dec.tokens.view(2, 1)], dim=1)
+
+
 def test_kvcache_decode_graph_replay_matches_eager():
     """The decode step captured once and replayed (tokens and lengths advanced
     on the device between replays) equals an eager decoder step by step."""
