@@ -168,7 +168,7 @@ typedef struct {
   int32_t dtype;               /* bf16 or fp16 */
   int32_t batch;
   int32_t heads_q;
-  int32_t heads_kv;            /* heads_q / heads_kv in {1, 2, 4, 8} */
+  int32_t heads_kv;            /* heads_q / heads_kv <= 32 (block_size >= 16), else in {1, 2, 4, 8} */
   int32_t head_dim;            /* multiple of 8, at most 128 */
   int32_t block_size;          /* power of two */
   int32_t num_blocks;

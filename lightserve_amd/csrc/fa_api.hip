@@ -120,11 +120,17 @@ DecodeSplit decode_split(const lsfa_decode_args* a) {
   DecodeSplit d;
   const int maxs = std::max(a->max_seq_len, 0);
   const long long units = std::max(1LL, (long long)a->batch * a->heads_kv);
-  // Splits of about 512 tokens while fewer than ~16 workgroups per CU exist:
-  // sequence lengths vary, and short splits keep the longest sequences from
-  // setting the tail.
+  // Lane-group kernel: splits of about 512 tokens while fewer than ~16
+  // workgroups per CU exist (sequence lengths vary, and short splits keep the
+  // longest sequences from setting the tail). MFMA kernel (one workgroup per
+  // CU): splits only below one workgroup per CU, of at least 4096 tokens, so
+  // that each workgroup's first-load latency is amortised.
+  const int g = a->heads_kv > 0 ? a->heads_q / a->heads_kv : 1;
+  const bool mfma = lsfa::decode_uses_mfma(g, std::max(0, log2_exact(std::max(1, a->block_size))));
+  const long long target = mfma ? 256 : 4096, min_split = mfma ? 4096 : 512;
   long long ns = 1;
-  if (units < 4096 && maxs > 512) ns = std::min<long long>((4096 + units - 1) / units, (maxs + 511) / 512);
+  if (units < target && maxs > min_split)
+    ns = std::min<long long>((target + units - 1) / units, (maxs + min_split - 1) / min_split);
   long long st = (maxs + ns - 1) / ns;
   st = std::max(64LL, (st + 63) / 64 * 64);
   const int shift = std::max(0, log2_exact(std::max(1, a->block_size)));
@@ -302,13 +308,16 @@ int lsfa_decode_check(const lsfa_decode_args* a) {
                 "max_blocks_per_seq=%d max_seq_len=%d)", a->batch, a->heads_q, a->heads_kv, a->num_blocks,
                 a->max_blocks_per_seq, a->max_seq_len);
   if (a->heads_q % a->heads_kv != 0) return fail(LSFA_ERR_INVALID, "heads_q (%d) is not a multiple of heads_kv (%d)", a->heads_q, a->heads_kv);
-  const int g = a->heads_q / a->heads_kv;
-  if (g != 1 && g != 2 && g != 4 && g != 8)
-    return fail(LSFA_ERR_UNSUPPORTED, "heads_q / heads_kv = %d; decode supports 1, 2, 4 and 8", g);
   if (a->head_dim < 8 || a->head_dim > 128 || a->head_dim % 8 != 0)
     return fail(LSFA_ERR_UNSUPPORTED, "decode head_dim must be a multiple of 8 in 8..128 (got %d)", a->head_dim);
   if (a->block_size < 1 || log2_exact(a->block_size) < 0)
     return fail(LSFA_ERR_UNSUPPORTED, "block_size must be a power of two (got %d)", a->block_size);
+  // Blocks of 16 tokens or more take the MFMA kernel (query heads are MFMA
+  // columns: up to 32 per KV head); smaller blocks the lane-group kernel.
+  const int g = a->heads_q / a->heads_kv;
+  if (a->block_size >= 16 ? g > 32 : (g != 1 && g != 2 && g != 4 && g != 8))
+    return fail(LSFA_ERR_UNSUPPORTED, "heads_q / heads_kv = %d; decode supports up to 32 with block_size >= 16, "
+                "else 1, 2, 4 and 8", g);
   if (!std::isfinite(a->sm_scale)) return fail(LSFA_ERR_INVALID, "sm_scale is not finite");
   if (a->batch == 0) return ok();
   if (!a->q || !a->k_cache || !a->v_cache || !a->o || !a->block_tables || !a->seq_lens)

@@ -191,6 +191,13 @@ struct BwdParams {
 
 // Paged-KV decode (one query token per sequence); strides in elements.
 constexpr int kDecodeMaxTableSlots = 512;  // block-table entries one split may span
+
+// Which decode kernel serves a group size Hq/Hkv and block size 2^shift: the
+// lane-group kernel for groups 1, 2, 4, 8; the MFMA kernel for other groups
+// (up to 32) with blocks of at least 16 tokens.
+inline __host__ __device__ bool decode_uses_mfma(int group, int block_shift) {
+  return block_shift >= 4 && group != 1 && group != 2 && group != 4 && group != 8;
+}
 struct DecodeParams {
   const void* q;       // [B, Hq, D]
   const void* kc;      // [num_blocks, block_size, Hkv, D]

@@ -265,6 +265,40 @@ def test_abi_rope_validation(built_library):
         _lib.rope(_rope_args(batch=-1), 0)
 
 
+def _decode_args(**kw):
+    base = dict(q=4096, k_cache=8192, v_cache=12288, o=16384, lse=None, block_tables=20480, seq_lens=24576,
+                workspace=None, workspace_bytes=0, q_stride=_lib._i64x3(1024, 128, 1),
+                k_stride=_lib._i64x4(16 * 2 * 128, 256, 128, 1), v_stride=_lib._i64x4(16 * 2 * 128, 256, 128, 1),
+                o_stride=_lib._i64x3(1024, 128, 1), lse_stride=_lib._i64x2(8, 1), block_table_stride=8,
+                dtype=_lib.DTYPE_BF16, batch=2, heads_q=8, heads_kv=2, head_dim=128, block_size=16, num_blocks=16,
+                max_blocks_per_seq=8, max_seq_len=128, sm_scale=0.088)
+    base.update(kw)
+    return _lib.DecodeArgs(**base)
+
+
+def test_abi_decode_validation(built_library):
+    """Host-only validation of lsfa_decode (fake, never dereferenced pointers):
+    group sizes up to 32 with blocks of 16 or more (the MFMA kernel), only
+    1/2/4/8 with smaller blocks (the lane-group kernel)."""
+    assert _lib.decode_check(_decode_args())[0] == 0
+    assert _lib.decode_check(_decode_args(heads_q=6))[0] == 0  # group of 3, 16-token blocks
+    assert _lib.decode_check(_decode_args(heads_q=64))[0] == 0  # group of 32
+    assert _lib.decode_check(_decode_args(block_size=4, k_stride=_lib._i64x4(4 * 256, 256, 128, 1),
+                                          v_stride=_lib._i64x4(4 * 256, 256, 128, 1)))[0] == 0
+    rc, msg = _lib.decode_check(_decode_args(heads_q=66))  # group of 33
+    assert rc == -2 and "heads_q / heads_kv" in msg
+    rc, msg = _lib.decode_check(_decode_args(heads_q=6, block_size=8))  # group of 3, small blocks
+    assert rc == -2 and "heads_q / heads_kv" in msg
+    rc, msg = _lib.decode_check(_decode_args(block_size=24))
+    assert rc == -2 and "power of two" in msg
+    rc, msg = _lib.decode_check(_decode_args(dtype=_lib.DTYPE_FP32))
+    assert rc == -2
+    rc, msg = _lib.decode_check(_decode_args(heads_q=7))
+    assert rc == -1 and "multiple" in msg
+    rc, msg = _lib.decode_check(_decode_args(seq_lens=None))
+    assert rc == -1 and "non-NULL" in msg
+
+
 def _prefill_args(**kw):
     base = dict(q=4096, k_cache=8192, v_cache=12288, o=16384, lse=None, cu_seqlens_q=20480, seq_lens_k=24576,
                 block_tables=28672, q_stride=_lib._i64x2(1024, 128), k_stride=_lib._i64x3(16 * 2 * 128, 256, 128),

@@ -4,10 +4,12 @@ The reference has no decode kernel (its engine documents it as missing,
 engine/README.md "No decode-shaped attention kernel"), so parity is against
 oracle.attention.paged_decode_reference (gather through the block table,
 then the closed-form attention), under the BASELINE gate (max-abs 2e-2,
-mean-abs 2e-3, lse 1e-3). Cases: GQA group sizes 1/2/4/8, head dims 32-128,
-block sizes 1/16/32, ragged and empty sequences, lengths at block
-boundaries, shuffled physical blocks, split and unsplit launches, and the
-device-side clamp of seq_lens to max_seq_len.
+mean-abs 2e-3, lse 1e-3). Two kernels are covered: the MFMA kernel (block
+sizes that are multiples of 16, any group size up to 32) and the lane-group
+kernel (smaller blocks, groups 1/2/4/8). Cases: GQA group sizes 1-32, head
+dims 32-128, block sizes 1/16/32/64, ragged and empty sequences, lengths at
+block and tile boundaries, shuffled physical blocks, split and unsplit
+launches, and the device-side clamp of seq_lens to max_seq_len.
 """
 import pytest
 import torch
@@ -60,7 +62,7 @@ def test_decode_small(gpu, hq, hkv, d, dtype):
     _check(*_make_case(lens, hq, hkv, d, 16, dtype, gpu, seed=hq + d), f"hq={hq} hkv={hkv} d={d}")
 
 
-@pytest.mark.parametrize("bs", [1, 32])
+@pytest.mark.parametrize("bs", [1, 32, 64])
 @pytest.mark.parametrize("d", [32, 96])
 def test_decode_block_sizes_and_padded_dims(gpu, bs, d):
     print(f"case decode bs={bs} d={d}", flush=True)
@@ -102,9 +104,20 @@ def test_decode_seq_lens_clamped_on_device(gpu):
     _check(q, kc, vc, table, sl_claimed, "clamp", max_seq_len=64, lens_ref=torch.tensor([40, 64, 64]))
 
 
+@pytest.mark.parametrize("hq,hkv,bs", [(12, 4, 16), (32, 2, 16), (32, 1, 64), (24, 8, 32)])
+def test_decode_mfma_group_sizes(gpu, hq, hkv, bs):
+    """Group sizes only the MFMA kernel takes (3, 16, 32), and 64-token blocks."""
+    lens = [1, 31, 32, 33, 0, 640, 2000, 129]
+    print(f"case decode groups hq={hq} hkv={hkv} bs={bs}", flush=True)
+    _check(*_make_case(lens, hq, hkv, 128, bs, torch.bfloat16, gpu, seed=hq + bs), f"hq={hq} hkv={hkv} bs={bs}")
+
+
 def test_decode_rejects_bad_arguments(gpu):
-    q, kc, vc, table, sl = _make_case([4], 6, 2, 64, 16, torch.bfloat16, gpu, seed=1)
-    with pytest.raises(RuntimeError, match="heads_q / heads_kv"):  # group of 3
+    q, kc, vc, table, sl = _make_case([4], 6, 2, 64, 8, torch.bfloat16, gpu, seed=1)
+    with pytest.raises(RuntimeError, match="heads_q / heads_kv"):  # group of 3 with 8-token blocks
+        paged_attention_decode(q.cuda(), kc.cuda(), vc.cuda(), table.cuda(), sl.cuda())
+    q, kc, vc, table, sl = _make_case([4], 64, 1, 64, 16, torch.bfloat16, gpu, seed=1)
+    with pytest.raises(RuntimeError, match="heads_q / heads_kv"):  # group of 64
         paged_attention_decode(q.cuda(), kc.cuda(), vc.cuda(), table.cuda(), sl.cuda())
     q, kc, vc, table, sl = _make_case([4], 4, 2, 64, 12, torch.bfloat16, gpu, seed=1)
     with pytest.raises(RuntimeError, match="power of two"):
