@@ -89,8 +89,8 @@ typedef struct {
  * least lsfa_bwd_workspace_size() bytes, 256-byte aligned; its contents on
  * entry do not matter and are scratch afterwards. The dq kernel's prologue
  * writes there what the reference's preprocess kernel computes (delta =
- * rowsum(dO * O), kernels/flash_attention_backward.py:202-229) plus
- * transposed copies of q and dout for the key-stationary kernel. dq/dk/dv
+ * rowsum(dO * O), kernels/flash_attention_backward.py:202-229) and
+ * L*log2(e) for the key-stationary kernel. dq/dk/dv
  * are written in the input dtype (no fp32 dq staging buffer and no atomics:
  * dq is produced by its own query-stationary kernel, so results are
  * deterministic). */

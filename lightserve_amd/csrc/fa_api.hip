@@ -76,29 +76,24 @@ int check_common(int dtype, int batch, int hq, int hkv, int nq, int nk, int d, f
   return LSFA_OK;
 }
 
-// Backward workspace: (lse*log2e, delta) pairs for every (b, h, query) and,
-// on the bf16/fp16 path, transposed copies of Q and dO. Queries are padded to
-// a multiple of the query-stationary tile (128, which the dq kernel writes
-// whole); each part starts on a 256-byte boundary.
+// Backward workspace: (lse*log2e, delta) pairs for every (b, h, query),
+// queries padded to a multiple of the query-stationary tile (128, which the
+// dq kernel writes whole).
 struct BwdWorkspace {
   int64_t nq_pad = 0;
-  uint64_t ld_off = 0, qt_off = 0, dot_off = 0, bytes = 0;
+  uint64_t ld_off = 0, bytes = 0;
 };
 
 uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
 BwdWorkspace bwd_workspace(int dtype, int batch, int heads, int nq, int head_dim) {
+  (void)dtype;
+  (void)head_dim;
   BwdWorkspace w;
   w.nq_pad = ((int64_t)nq + 127) / 128 * 128;
   const uint64_t rows = (uint64_t)batch * heads * w.nq_pad;
   w.ld_off = 0;
   w.bytes = align256(rows * 8);
-  if (dtype != LSFA_DTYPE_FP32) {
-    const uint64_t tb = align256(rows * padded_dim(head_dim) * 2);
-    w.qt_off = w.bytes;
-    w.dot_off = w.bytes + tb;
-    w.bytes += 2 * tb;
-  }
   return w;
 }
 
@@ -268,12 +263,6 @@ int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
   p.ld = reinterpret_cast<float*>(ws + w.ld_off);
   p.sldh = 2 * w.nq_pad;
   p.sldb = (int64_t)a->heads_q * p.sldh;
-  if (a->dtype != LSFA_DTYPE_FP32) {
-    p.qt = ws + w.qt_off;
-    p.dot = ws + w.dot_off;
-    p.sth = (int64_t)padded_dim(a->head_dim) * w.nq_pad;
-    p.stb = (int64_t)a->heads_q * p.sth;
-  }
   p.sqb = a->q_stride[0]; p.sqh = a->q_stride[1]; p.sqn = a->q_stride[2]; p.sqd = a->q_stride[3];
   p.skb = a->k_stride[0]; p.skh = a->k_stride[1]; p.skn = a->k_stride[2]; p.skd = a->k_stride[3];
   p.svb = a->v_stride[0]; p.svh = a->v_stride[1]; p.svn = a->v_stride[2]; p.svd = a->v_stride[3];

@@ -12,10 +12,9 @@
 // a dq workspace, :323-325, followed by a cast, :382), the work is split into
 //   fa_bwd_dq_kernel   : query-stationary. Its prologue does the reference's
 //                        preprocess (:341-350): delta and L*log2(e) per query
-//                        row into the workspace, plus transposed copies of Q
-//                        and dO whose query order matches the MFMA register
-//                        layout of P and dS. Then dQ = scale * dS K over all
-//                        visible key tiles, stored straight in the input dtype;
+//                        row into the workspace. Then dQ = scale * dS K over
+//                        all visible key tiles, stored straight in the input
+//                        dtype;
 //   fa_bwd_dkdv_kernel : key-stationary; dK, dV over all visible query tiles
 //                        (runs after the dq kernel, which feeds it).
 // Both kernels recompute S and dP. There are no atomics and no fp32 dq
@@ -25,16 +24,6 @@
 namespace lsfa {
 
 constexpr float kLog2eB = 1.4426950408889634f;
-
-// Stored position of tile-local query q in a transposed Q/dO row (and the
-// query held at stored position q: bits 2 and 3 swap, an involution). The 8
-// queries one lane half feeds to a 32x32x16 MFMA from P or dS,
-// 16*ks + 8*(s/4) + 4*half + s%4 for s = 0..7, then sit in 16 contiguous bytes.
-__device__ __forceinline__ int tpos(int q) { return (q & ~12) | ((q & 4) << 1) | ((q & 8) >> 1); }
-
-// 16-byte column swizzle of a transposed [DP][64] tile (128-byte rows): any
-// 16 consecutive rows read at one logical column hit distinct bank groups.
-__device__ __forceinline__ int tswz(int d) { return (d & 7) ^ ((d >> 3) & 1); }
 
 // ---------------------------------------------------------------------------
 // dQ. Workgroup = 4 waves x 32 query rows, at most 256 registers
@@ -106,12 +95,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   // go to LDS (rows past nq and columns past D as zero), then
   //   - Q^T and dO^T B operands of this kernel come from LDS;
   //   - delta = rowsum(dO * O) and L*log2e are written to the workspace for
-  //     the dK/dV kernel;
-  //   - the transposed, query-permuted copies of Q and dO the dK/dV kernel
-  //     reads are written to the workspace. The transpose reads below return,
-  //     for lane (d = 32*dt + l32, hh) and query step ks, queries
-  //     16*ks + 8*(s/4) + 4*hh + s%4 (s = 0..7): stored positions
-  //     16*ks + 8*hh + s of the workspace layout.
+  //     the dK/dV kernel.
   constexpr int TB = BM * DP * 2;  // bytes of one 128-row tile
   static_assert(2 * TB <= 4 * TILE * 2, "Q/dO tiles must fit in the K/V buffers");
   {
@@ -157,26 +141,6 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
     v.x = l2;
     v.y = delta;
     *(float2*)(p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 2 * (int64_t)qrow) = v;
-  }
-  {
-    constexpr int KS = BM / 16, UNITS = 2 * DT * KS;
-    T* Qt = (T*)p.qt + (int64_t)b * p.stb + (int64_t)h * p.sth + q0 + 8 * hh;
-    T* dOt = (T*)p.dot + (int64_t)b * p.stb + (int64_t)h * p.sth + q0 + 8 * hh;
-#pragma unroll
-    for (int u0 = 0; u0 < UNITS; u0 += NW) {
-      const int u = u0 + wave;
-      const int tsel = u / (DT * KS), dt = (u / KS) % DT, ks = u % KS;
-      const LDS_AS char* base = sm + tsel * TB + ks * 16 * DP * 2;
-      int o0 = 0, o1 = 0;
-#pragma unroll
-      for (int i = 0; i < DT; ++i)
-        if (i == dt) {
-          o0 = troff[i][0];
-          o1 = troff[i][1];
-        }
-      const X8 a = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(base + o0)), lds_read_tr((const LDS_AS T*)(base + o1)));
-      *(X8*)((tsel ? dOt : Qt) + (int64_t)(32 * dt + l32) * p.nq_pad + 16 * ks) = a;
-    }
   }
   __syncthreads();  // the K/V tiles below reuse the Q/dO buffers
 
@@ -295,16 +259,17 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 // dK, dV. Workgroup = 8 waves (two per SIMD, at most 256 registers each)
 // over 128 keys; K and V of those keys stay in LDS for the whole kernel.
 // Every operand reaches LDS with buffer_load ... lds (no register staging):
-// per 64-query tile, the row-major Q/dO tile (with L*log2e and delta) and
-// the transposed Q^T/dO^T tile from the workspace. The two halves are
-// prefetched in alternation: the transposed tile streams in while S and dP
-// are computed, the next row tile while dV and dK accumulate. Wave w owns
-// keys 32*(w%4)..+31 and query rows 32*(w/4)..+31 of every tile:
+// per 64-query tile, the row-major Q/dO tile with L*log2e and delta, in two
+// stages. Wave w owns keys 32*(w%4)..+31 and query rows 32*(w/4)..+31 of
+// every tile:
 //   S  = Q K^T            A = Q rows (LDS),   B = K rows (LDS)
 //   dP = dO V^T           A = dO rows (LDS),  B = V rows (LDS)
 //   P  = exp2(S*scale*log2e - L*log2e), dS = P (dP - delta)
-//   dV^T += dO^T P        A = dO^T (LDS),     B = P  (registers)
-//   dK^T += Q^T dS        A = Q^T (LDS),      B = dS (registers)
+//   dV^T += dO^T P        A = dO^T (transpose reads of the dO rows), B = P
+//   dK^T += Q^T dS        A = Q^T (transpose reads of the Q rows),   B = dS
+// The two waves of a SIMD (same keys, the two query halves) run half a tile
+// apart (see the loop), so one's softmax VALU work overlaps the other's
+// dV/dK MFMAs.
 // The two query halves' partial dK/dV are summed through LDS at the end.
 // Query rows beyond the sequence have L = +inf in the workspace (written by
 // the dq kernel's prologue), so their P is exactly 0; head-dim columns at or
@@ -318,16 +283,15 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   constexpr int KSTEPS = DP / 16, DT = DP / 32;
   constexpr int KV_B = BNK * DP * 2;  // bytes of K (or V)
   constexpr int R_B = BMQ * DP * 2;   // bytes of a row-major Q (or dO) tile
-  constexpr int T_B = DP * BMQ * 2;   // bytes of a transposed Q (or dO) tile
-  constexpr int OFF_K = 0, OFF_V = KV_B, OFF_Q = 2 * KV_B, OFF_DO = OFF_Q + R_B;
-  constexpr int OFF_QT = OFF_DO + R_B, OFF_DOT = OFF_QT + T_B, OFF_LD = OFF_DOT + T_B;
-  constexpr int LDS_B = OFF_LD + BMQ * 8;
+  // Two row stages, each Q | dO | (L*log2e, delta) pairs, 1 KB aligned.
+  constexpr int RS_B = 2 * R_B + 1024;
+  constexpr int OFF_K = 0, OFF_V = KV_B, OFF_R = 2 * KV_B;
+  constexpr int LDS_B = OFF_R + 2 * RS_B;
   constexpr int NG = 2 * DT * 4;  // f32x4 groups of dK^T and dV^T per lane
   static_assert((NW / 2) * NG * 64 * 16 <= LDS_B, "epilogue does not fit in LDS");
   constexpr int CKV = 2 * KV_B / 1024 / NW;  // 1 KB chunks per wave: K|V
   constexpr int CR = 2 * R_B / 1024 / NW;    //                        Q|dO rows
-  constexpr int CT = 2 * T_B / 1024 / NW;    //                        Q^T|dO^T
-  static_assert(CKV >= 1 && CR >= 1 && CT >= 1, "tile too small for the workgroup");
+  static_assert(CKV >= 1 && CR >= 1, "tile too small for the workgroup");
 
   __shared__ __attribute__((aligned(1024))) char sm_raw[LDS_B];
   LDS_AS char* sm = (LDS_AS char*)sm_raw;
@@ -336,7 +300,7 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
   const int kb = wave & 3, qh = wave >> 2;
-  const bool w_hi = wave >= NW / 2;  // waves 4..7 load V, dO, dO^T; 0..3 load K, Q, Q^T
+  const bool w_hi = wave >= NW / 2;  // waves 4..7 load V and dO; 0..3 load K and Q
   int bh, kt;
   map_tile(p.num_tiles, gridDim.x, bh, kt, false);  // low key tiles see the most queries
   const int b = bh / p.H, h = bh - b * p.H;
@@ -348,8 +312,6 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh + (int64_t)k0 * p.svn;
   const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
   const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
-  const T* Qt = (const T*)p.qt + (int64_t)b * p.stb + (int64_t)h * p.sth;
-  const T* dOt = (const T*)p.dot + (int64_t)b * p.stb + (int64_t)h * p.sth;
   const float* LD = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh;
 
   // Lane byte offset of row-major chunk lc (tile rows of 2*DP bytes): lane t
@@ -376,54 +338,44 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     }
   }
 
-  int rvo[CR], tvo[CT];
+  int rvo[CR];
 #pragma unroll
   for (int i = 0; i < CR; ++i) rvo[i] = row_voff((wave % (NW / 2)) * CR + i, w_hi ? p.sdon : p.sqn);
-#pragma unroll
-  for (int i = 0; i < CT; ++i) {
-    const int byte = ((wave % (NW / 2)) * CT + i) * 1024 + lane * 16;
-    const int d = byte / (BMQ * 2);
-    const int seg = ((byte % (BMQ * 2)) / 16) ^ tswz(d);
-    tvo[i] = d * p.nq_pad * 2 + seg * 16;
-  }
 
   // (Offset arrays go in as pointers and lambda results are hoisted into
   // locals: an array-reference lambda parameter, or a lambda call inside a
   // builtin's argument list, makes clang's host pass silently drop the
   // kernel's launch stub.)
-  auto load_rows = [&](int t, const int* vo) {
+  auto load_rows = [&](int t, int stage, const int* vo) {
     const int q0 = t * BMQ;
     const int rows = min(nq - q0, BMQ);
     const int64_t sn = w_hi ? p.sdon : p.sqn;
     const __amdgpu_buffer_rsrc_t rs = tile_rsrc((w_hi ? dO : Q) + (int64_t)q0 * sn, (int)(rows * sn * 2));
+    LDS_AS char* base = sm + OFF_R + stage * RS_B;
 #pragma unroll
     for (int i = 0; i < CR; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(sm + OFF_Q + (wave * CR + i) * 1024), 16, vo[i],
-                                               0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(base + (wave * CR + i) * 1024), 16, vo[i], 0, 0, 0);
     if (wave == 0 && lane < BMQ * 8 / 16) {
       const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(LD + 2 * (int64_t)q0, BMQ * 8);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (LDS_AS void*)(sm + OFF_LD), 16, lane * 16, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (LDS_AS void*)(base + 2 * R_B), 16, lane * 16, 0, 0, 0);
     }
-  };
-  auto load_trans = [&](int t, const int* vo) {
-    const T* base = (w_hi ? dOt : Qt) + t * BMQ;
-    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base, (int)((int64_t)(DP - 1) * p.nq_pad * 2 + BMQ * 2));
-#pragma unroll
-    for (int i = 0; i < CT; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(sm + OFF_QT + (wave * CT + i) * 1024), 16, vo[i],
-                                               0, 0, 0);
   };
 
   // LDS read offsets. Row-major tiles: the swizzle depends on row & 15, so
-  // the wave's 32-row blocks are plain byte offsets. Transposed tiles: row
-  // d = 32*dt + l32, stored column (4*qh + 2*ks + hh) ^ tswz(l32).
+  // the wave's 32-row blocks are plain byte offsets; Q^T and dO^T come from
+  // the same row-major tiles through transpose reads (16-query steps).
   int roff[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) roff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
   const int qrow_b = 32 * qh * DP * 2, krow_b = 32 * kb * DP * 2;
-  int toffs[2];
+  const int tr_row = 4 * hh + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int troff[DT][2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) toffs[ks] = l32 * (BMQ * 2) + (((4 * qh + 2 * ks + hh) ^ tswz(l32)) << 4);
+  for (int dt = 0; dt < DT; ++dt) {
+    troff[dt][0] = swz_off<DP>(tr_row, 32 * dt + tr_col) * 2;
+    troff[dt][1] = swz_off<DP>(tr_row + 8, 32 * dt + tr_col) * 2;
+  }
 
   f32x16 dk[DT], dv[DT];
 #pragma unroll
@@ -436,25 +388,31 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   int t_begin = 0;
   if (CAUSAL) t_begin = max(0, k0 - off) / BMQ;  // first tile holding a query that sees key k0
   const int kcol = k0 + 32 * kb + l32;            // this lane's key
+  const int n_t = max(0, n_qt - t_begin);
 
-  if (t_begin < n_qt) load_rows(t_begin, rvo);
-  for (int t = t_begin; t < n_qt; ++t) {
+  // The two query halves run half a tile apart, so that on every SIMD one
+  // wave computes S, dP and the softmax (MFMA then VALU) while its partner
+  // (same keys, other query half) accumulates dV and dK (MFMA only). Step
+  // 2i of a wave is phase 1 of its i-th tile, step 2i+1 phase 2; the qh = 1
+  // waves are one step behind, so tile i's rows are read in segments 2i ..
+  // 2i+2 and tile i+2 (same row stage) loads during segment 2i+3.
+  X8 P0{}, P1{}, G0{}, G1{};  // phase 1 -> phase 2 of the same tile
+  auto phase1 = [&](int t, const LDS_AS char* st) {
     const int q0 = t * BMQ;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // row tile t landed; everyone is done with the transposed tile t-1
-    load_trans(t, tvo);
-
     f32x16 s = f32x16{}, dp = f32x16{};
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
-      s = mfma32(*(const LDS_AS X8*)(sm + OFF_Q + qrow_b + roff[kk]), *(const LDS_AS X8*)(sm + OFF_K + krow_b + roff[kk]), s);
-      dp = mfma32(*(const LDS_AS X8*)(sm + OFF_DO + qrow_b + roff[kk]), *(const LDS_AS X8*)(sm + OFF_V + krow_b + roff[kk]), dp);
+      s = mfma32(*(const LDS_AS X8*)(st + qrow_b + roff[kk]), *(const LDS_AS X8*)(sm + OFF_K + krow_b + roff[kk]), s);
+      dp = mfma32(*(const LDS_AS X8*)(st + R_B + qrow_b + roff[kk]),
+                  *(const LDS_AS X8*)(sm + OFF_V + krow_b + roff[kk]), dp);
     }
+    __builtin_amdgcn_s_setprio(0);
     // Register i holds query q0 + 32*qh + 8*(i/4) + 4*hh + i%4 of key kcol;
     // (L*log2e, delta) of those four consecutive queries are two 16-byte reads.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const LDS_AS f32x4* ldp = (const LDS_AS f32x4*)(sm + OFF_LD + (32 * qh + 8 * j + 4 * hh) * 8);
+      const LDS_AS f32x4* ldp = (const LDS_AS f32x4*)(st + 2 * R_B + (32 * qh + 8 * j + 4 * hh) * 8);
       const f32x4 a = ldp[0], c = ldp[1];
       const float l2v[4] = {a[0], a[2], c[0], c[2]};
       const float dlv[4] = {a[1], a[3], c[1], c[3]};
@@ -475,20 +433,58 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
         dp[i] = m ? 0.f : dp[i];
       }
     }
-    const X8 P0 = pack8<T>(s, 0), P1 = pack8<T>(s, 8);
-    const X8 G0 = pack8<T>(dp, 0), G1 = pack8<T>(dp, 8);
-
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // transposed tile t landed; everyone is done with row tile t
-    if (t + 1 < n_qt) load_rows(t + 1, rvo);
-
+    P0 = pack8<T>(s, 0);
+    P1 = pack8<T>(s, 8);
+    G0 = pack8<T>(dp, 0);
+    G1 = pack8<T>(dp, 8);
+  };
+  auto phase2 = [&](const LDS_AS char* st) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const int tb = dt * 32 * BMQ * 2;
-      dv[dt] = mfma32(*(const LDS_AS X8*)(sm + OFF_DOT + tb + toffs[0]), P0, dv[dt]);
-      dk[dt] = mfma32(*(const LDS_AS X8*)(sm + OFF_QT + tb + toffs[0]), G0, dk[dt]);
-      dv[dt] = mfma32(*(const LDS_AS X8*)(sm + OFF_DOT + tb + toffs[1]), P1, dv[dt]);
-      dk[dt] = mfma32(*(const LDS_AS X8*)(sm + OFF_QT + tb + toffs[1]), G1, dk[dt]);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const LDS_AS char* qb = st + (32 * qh + 16 * ks) * DP * 2;
+        const X8 ado = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(qb + R_B + troff[dt][0])),
+                                    lds_read_tr((const LDS_AS T*)(qb + R_B + troff[dt][1])));
+        const X8 aq = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(qb + troff[dt][0])),
+                                   lds_read_tr((const LDS_AS T*)(qb + troff[dt][1])));
+        dv[dt] = mfma32(ado, ks == 0 ? P0 : P1, dv[dt]);
+        dk[dt] = mfma32(aq, ks == 0 ? G0 : G1, dk[dt]);
+      }
+    }
+  };
+
+  if (n_t > 0) load_rows(t_begin, 0, rvo);
+  if (n_t > 1) load_rows(t_begin + 1, 1, rvo);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // One loop per query half (wave-uniform branch outside the loops), so each
+  // phase's registers are live only in its own segment; both loops pass the
+  // same 2*n_t + 1 barriers. Segment 2i+1 (i >= 1) loads tile i+1 into the
+  // stage tile i-1 used.
+  auto seg_end = [&]() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  };
+  if (qh == 0) {
+    for (int i = 0; i < n_t; ++i) {
+      const LDS_AS char* st = sm + OFF_R + (i & 1) * RS_B;
+      phase1(t_begin + i, st);  // segment 2i
+      seg_end();
+      if (i >= 1 && i + 1 < n_t) load_rows(t_begin + i + 1, (i + 1) & 1, rvo);  // segment 2i+1
+      phase2(st);
+      seg_end();
+    }
+    seg_end();  // segment 2*n_t: the other half's last phase 2
+  } else {
+    seg_end();  // segment 0: the other half's first phase 1
+    for (int i = 0; i < n_t; ++i) {
+      const LDS_AS char* st = sm + OFF_R + (i & 1) * RS_B;
+      if (i >= 1 && i + 1 < n_t) load_rows(t_begin + i + 1, (i + 1) & 1, rvo);  // segment 2i+1
+      phase1(t_begin + i, st);
+      seg_end();
+      phase2(st);  // segment 2i+2
+      seg_end();
     }
   }
 

@@ -165,13 +165,8 @@ struct BwdParams {
   // Workspace written by the dq kernel's prologue:
   //   ld  : (lse * log2(e), delta) pairs, element (b, h, q) at b*sldb + h*sldh + 2q;
   //         +inf stands in for lse where a row sees no key or q >= Nq
-  //   qt, dot : Q^T and dO^T in the input dtype (bf16/fp16 path only), element
-  //         (b, h, d, pos) at b*stb + h*sth + d*nq_pad + pos, where stored
-  //         position pos holds query pos with bits 2 and 3 swapped
   float* ld;
-  void* qt;
-  void* dot;
-  int64_t sldb, sldh, stb, sth;
+  int64_t sldb, sldh;
   int nq_pad;  // Nq rounded up to the query-stationary tile (128)
   int64_t sqb, sqh, sqn;
   int64_t skb, skh, skn;

@@ -196,8 +196,7 @@ def test_abi_backward_validation(built_library):
 
 def test_abi_backward_workspace(built_library):
     """Workspace size: (L*log2e, delta) fp32 pairs for every (b, h, query) with
-    queries padded to 128, plus transposed bf16/fp16 copies of q and dout at the
-    padded head dim; each part 256-byte aligned. Too small or misaligned
+    queries padded to 128, 256-byte aligned. Too small or misaligned
     workspaces are rejected before any launch."""
     st = _lib._i64x4(2048, 512, 64, 1)
     args = _lib.BwdArgs(q=16, k=32, v=48, o=64, dout=80, lse=96, dq=112, dk=128, dv=144, workspace=4096,
@@ -208,7 +207,7 @@ def test_abi_backward_workspace(built_library):
                         heads_q=4, heads_kv=4, seqlen_q=8, seqlen_k=8, head_dim=64, causal=1,
                         sm_scale=0.125, reserved=0)
     rows = 1 * 4 * 128
-    expected = rows * 8 + 2 * rows * 64 * 2
+    expected = rows * 8
     assert _lib.bwd_workspace_size(args) == expected
     args.seqlen_q = 128
     assert _lib.bwd_workspace_size(args) == expected
