@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define LSFA_ABI_VERSION 6
+#define LSFA_ABI_VERSION 7
 
 typedef enum {
   LSFA_DTYPE_FP32 = 0,
@@ -292,6 +292,60 @@ typedef struct {
   int32_t reserved;
 } lsfa_prefill_paged_args;
 
+/* Skinny GEMM for decode-time projections: y[M, N] = x[M, K] @ w[K, N] with
+ * M <= 8, w in the reference model's [in, out] row-major weight layout
+ * (model/minimal_llama.py: every Linear is x @ w), bf16 or fp16, fp32
+ * accumulate, one rounding. The reference calls its tiled GEMM for these
+ * (kernels/tiled_matmul.py:135-164, through model/minimal_llama.py:178-182);
+ * this entry point serves the rows-per-call of a decode step, where a GEMM's
+ * tiles are mostly empty and the product is one HBM pass over w.
+ *   x [M, K], y [M, N]: row strides in elements, columns contiguous
+ *   w [K, N]: row stride w_stride >= N, columns contiguous; N % 8 == 0
+ *   workspace: lsfa_gemv_workspace_size() bytes (0 when K needs no split),
+ *   256-byte aligned: the first LSFA_GEMV_COUNTER_BYTES hold int32 arrival
+ *   counters (16 per 256 columns of y, hence n <= 1048576), then the fp32
+ *   partial sums of the K-splits. The counter bytes must be zero the first
+ *   time a workspace is used; every call leaves them zero, so calls in stream
+ *   order, of any shape, may reuse one workspace. Calls that can run at the
+ *   same time need workspaces of their own. */
+#define LSFA_GEMV_COUNTER_BYTES 262144
+typedef struct {
+  const void* x;
+  const void* w;
+  void* y;
+  void* workspace;
+  uint64_t workspace_bytes;
+  int64_t x_stride;
+  int64_t w_stride;
+  int64_t y_stride;
+  int32_t dtype;
+  int32_t m;
+  int32_t k;
+  int32_t n;
+} lsfa_gemv_args;
+
+/* Grouped skinny GEMM: y_i = x @ w_i for count <= LSFA_GEMV_MAX_GROUP weight
+ * matrices that share x (and so K), e.g. a decoder's q/k/v or gate/up
+ * projections, as one launch over their concatenated columns. Each w_i / y_i
+ * follows the rules of lsfa_gemv_args; the workspace (counters, then partials
+ * of all columns) follows them for n = n[0] + ... + n[count-1]. */
+#define LSFA_GEMV_MAX_GROUP 4
+typedef struct {
+  const void* x;
+  void* workspace;
+  uint64_t workspace_bytes;
+  int64_t x_stride;
+  const void* w[LSFA_GEMV_MAX_GROUP];
+  void* y[LSFA_GEMV_MAX_GROUP];
+  int64_t w_stride[LSFA_GEMV_MAX_GROUP];
+  int64_t y_stride[LSFA_GEMV_MAX_GROUP];
+  int32_t n[LSFA_GEMV_MAX_GROUP];
+  int32_t dtype;
+  int32_t m;
+  int32_t k;
+  int32_t count;
+} lsfa_gemv_group_args;
+
 /* ABI version of the loaded library (LSFA_ABI_VERSION). */
 int lsfa_abi_version(void);
 
@@ -345,6 +399,22 @@ int lsfa_prefill_paged_check(const lsfa_prefill_paged_args* args);
  * forward kernel of lsfa_fwd with K/V tiles gathered through the block
  * tables. No reference counterpart. */
 int lsfa_prefill_paged(const lsfa_prefill_paged_args* args, void* stream);
+
+/* Host-only validation of skinny-GEMM arguments; never touches the GPU. */
+int lsfa_gemv_check(const lsfa_gemv_args* args);
+
+/* Workspace bytes lsfa_gemv needs (m, k and n matter); no GPU work. */
+int lsfa_gemv_workspace_size(const lsfa_gemv_args* args, uint64_t* bytes);
+
+/* y = x @ w for m <= 8 rows (see lsfa_gemv_args): one launch on the stream,
+ * a K-split pass over w whose last-arriving workgroup per column block sums
+ * the splits (in split order: deterministic) and rounds once into y. */
+int lsfa_gemv(const lsfa_gemv_args* args, void* stream);
+
+/* The grouped form (lsfa_gemv_group_args): validation, workspace size, launch. */
+int lsfa_gemv_group_check(const lsfa_gemv_group_args* args);
+int lsfa_gemv_group_workspace_size(const lsfa_gemv_group_args* args, uint64_t* bytes);
+int lsfa_gemv_group(const lsfa_gemv_group_args* args, void* stream);
 
 /* Host-only validation of RMSNorm arguments; never touches the GPU. */
 int lsfa_rmsnorm_check(const lsfa_rmsnorm_args* args);

@@ -13,7 +13,7 @@ import torch
 
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
 TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}
@@ -24,7 +24,9 @@ EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "ls
                     "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd",
                     "lsfa_decode_check", "lsfa_decode_workspace_size", "lsfa_decode",
                     "lsfa_rope_check", "lsfa_rope", "lsfa_rmsnorm_check", "lsfa_rmsnorm",
-                    "lsfa_prefill_paged_check", "lsfa_prefill_paged")
+                    "lsfa_prefill_paged_check", "lsfa_prefill_paged",
+                    "lsfa_gemv_check", "lsfa_gemv_workspace_size", "lsfa_gemv",
+                    "lsfa_gemv_group_check", "lsfa_gemv_group_workspace_size", "lsfa_gemv_group")
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -98,6 +100,31 @@ class PrefillPagedArgs(ctypes.Structure):
     ]
 
 
+class GemvArgs(ctypes.Structure):
+    """Mirror of lsfa_gemv_args."""
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("y", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64),
+        ("x_stride", ctypes.c_int64), ("w_stride", ctypes.c_int64), ("y_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("m", ctypes.c_int32), ("k", ctypes.c_int32), ("n", ctypes.c_int32),
+    ]
+
+
+GEMV_MAX_GROUP = 4
+
+
+class GemvGroupArgs(ctypes.Structure):
+    """Mirror of lsfa_gemv_group_args."""
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64),
+        ("x_stride", ctypes.c_int64),
+        ("w", ctypes.c_void_p * GEMV_MAX_GROUP), ("y", ctypes.c_void_p * GEMV_MAX_GROUP),
+        ("w_stride", ctypes.c_int64 * GEMV_MAX_GROUP), ("y_stride", ctypes.c_int64 * GEMV_MAX_GROUP),
+        ("n", ctypes.c_int32 * GEMV_MAX_GROUP),
+        ("dtype", ctypes.c_int32), ("m", ctypes.c_int32), ("k", ctypes.c_int32), ("count", ctypes.c_int32),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -148,18 +175,24 @@ def load():
         lib.lsfa_last_error.argtypes = []
         for name, struct in (("lsfa_fwd_check", FwdArgs), ("lsfa_bwd_check", BwdArgs),
                              ("lsfa_decode_check", DecodeArgs), ("lsfa_rope_check", RopeArgs),
-                             ("lsfa_rmsnorm_check", RmsNormArgs), ("lsfa_prefill_paged_check", PrefillPagedArgs)):
+                             ("lsfa_rmsnorm_check", RmsNormArgs), ("lsfa_prefill_paged_check", PrefillPagedArgs),
+                             ("lsfa_gemv_check", GemvArgs), ("lsfa_gemv_group_check", GemvGroupArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct)]
         for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_decode", DecodeArgs),
                              ("lsfa_rope", RopeArgs), ("lsfa_rmsnorm", RmsNormArgs),
-                             ("lsfa_prefill_paged", PrefillPagedArgs)):
+                             ("lsfa_prefill_paged", PrefillPagedArgs), ("lsfa_gemv", GemvArgs),
+                             ("lsfa_gemv_group", GemvGroupArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
         lib.lsfa_bwd_workspace_size.restype = ctypes.c_int
         lib.lsfa_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdArgs), ctypes.POINTER(ctypes.c_uint64)]
+        lib.lsfa_gemv_group_workspace_size.restype = ctypes.c_int
+        lib.lsfa_gemv_group_workspace_size.argtypes = [ctypes.POINTER(GemvGroupArgs), ctypes.POINTER(ctypes.c_uint64)]
+        lib.lsfa_gemv_workspace_size.restype = ctypes.c_int
+        lib.lsfa_gemv_workspace_size.argtypes = [ctypes.POINTER(GemvArgs), ctypes.POINTER(ctypes.c_uint64)]
         lib.lsfa_decode_workspace_size.restype = ctypes.c_int
         lib.lsfa_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_uint64)]
         version = lib.lsfa_abi_version()
@@ -220,6 +253,40 @@ def prefill_paged_check(args):
 
 def prefill_paged(args, stream):
     _raise_on(load().lsfa_prefill_paged(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_prefill_paged")
+
+
+def gemv_check(args):
+    """Host-only validation (no GPU access); returns (status, message)."""
+    rc = load().lsfa_gemv_check(ctypes.byref(args))
+    return rc, load().lsfa_last_error().decode(errors="replace")
+
+
+def gemv_workspace_size(args):
+    """Bytes of device workspace lsfa_gemv needs (host only)."""
+    n = ctypes.c_uint64(0)
+    _raise_on(load().lsfa_gemv_workspace_size(ctypes.byref(args), ctypes.byref(n)), "lsfa_gemv_workspace_size")
+    return n.value
+
+
+def gemv(args, stream):
+    _raise_on(load().lsfa_gemv(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_gemv")
+
+
+def gemv_group_check(args):
+    """Host-only validation (no GPU access); returns (status, message)."""
+    rc = load().lsfa_gemv_group_check(ctypes.byref(args))
+    return rc, load().lsfa_last_error().decode(errors="replace")
+
+
+def gemv_group_workspace_size(args):
+    n = ctypes.c_uint64(0)
+    _raise_on(load().lsfa_gemv_group_workspace_size(ctypes.byref(args), ctypes.byref(n)),
+              "lsfa_gemv_group_workspace_size")
+    return n.value
+
+
+def gemv_group(args, stream):
+    _raise_on(load().lsfa_gemv_group(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_gemv_group")
 
 
 def rope_check(args):

@@ -19,6 +19,8 @@ hipError_t bwd_f32(const BwdParams& p, int dp, bool causal, hipStream_t s);
 hipError_t decode_gqa(const DecodeParams& p, bool is_bf16, int dp, hipStream_t s);
 hipError_t rope_inplace(const RopeParams& p, int dtype, hipStream_t s);
 hipError_t add_rmsnorm(const NormParams& p, int dtype, bool vec, hipStream_t s);
+hipError_t gemv(const GemvParams& p, bool is_bf16, hipStream_t s);
+int gemv_capacity(int m);
 }  // namespace lsfa
 
 namespace {
@@ -443,6 +445,146 @@ int lsfa_prefill_paged(const lsfa_prefill_paged_args* a, void* stream) {
                                  reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "paged prefill launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+// Skinny GEMM split: about 1024 workgroups (256 columns x one K-range each)
+// with K-ranges of at least 64 rows (multiples of 8) and at most what keeps
+// x's range within 32 KB of LDS at the kernel's row capacity (2048 rows up to
+// 4 rows, 1024 at 8). Workspace (only with more than one split): the int32
+// arrival counters, 16 per 256-column block, in a region of fixed size
+// (LSFA_GEMV_COUNTER_BYTES, so that no call's partials overlap another call's
+// counters in a shared workspace), then the fp32 partials [splits][m][n].
+struct GemvSplit {
+  int kc = 8, splits = 1;
+  uint64_t counter_bytes = 0, bytes = 0;
+};
+
+GemvSplit gemv_split(long long M, long long K, long long N) {
+  GemvSplit g;
+  M = std::max(M, 0LL); K = std::max(K, 0LL); N = std::max(N, 0LL);
+  const long long col_blocks = std::max(1LL, (N + 255) / 256);
+  const long long kc_max = std::min(2048LL, 8192LL / lsfa::gemv_capacity((int)std::min(std::max(M, 1LL), 8LL)));
+  long long splits = std::max(1LL, std::min((1024 + col_blocks - 1) / col_blocks, (K + 63) / 64));
+  long long kc = std::max(8LL, ((K + splits - 1) / splits + 7) / 8 * 8);
+  kc = std::min(kc, kc_max);
+  splits = std::max(1LL, (K + kc - 1) / kc);
+  g.kc = (int)kc;
+  g.splits = (int)splits;
+  if (splits > 1) {
+    g.counter_bytes = LSFA_GEMV_COUNTER_BYTES;
+    g.bytes = g.counter_bytes + align256((uint64_t)splits * M * N * 4);
+  }
+  return g;
+}
+
+lsfa_gemv_group_args gemv_as_group(const lsfa_gemv_args* a) {
+  lsfa_gemv_group_args gr;
+  memset(&gr, 0, sizeof(gr));
+  gr.x = a->x; gr.workspace = a->workspace; gr.workspace_bytes = a->workspace_bytes; gr.x_stride = a->x_stride;
+  gr.w[0] = a->w; gr.y[0] = a->y; gr.w_stride[0] = a->w_stride; gr.y_stride[0] = a->y_stride; gr.n[0] = a->n;
+  gr.dtype = a->dtype; gr.m = a->m; gr.k = a->k; gr.count = 1;
+  return gr;
+}
+
+long long gemv_total_n(const lsfa_gemv_group_args* a) {
+  long long n = 0;
+  for (int i = 0; i < std::min(std::max(a->count, 0), LSFA_GEMV_MAX_GROUP); ++i) n += std::max(a->n[i], 0);
+  return n;
+}
+
+int lsfa_gemv_group_check(const lsfa_gemv_group_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  if (a->dtype != LSFA_DTYPE_FP16 && a->dtype != LSFA_DTYPE_BF16)
+    return fail(a->dtype == LSFA_DTYPE_FP32 ? LSFA_ERR_UNSUPPORTED : LSFA_ERR_INVALID,
+                "gemv supports bf16 and fp16 (dtype %d)", a->dtype);
+  if (a->count < 1 || a->count > LSFA_GEMV_MAX_GROUP)
+    return fail(LSFA_ERR_INVALID, "count must be 1..%d (count=%d)", LSFA_GEMV_MAX_GROUP, a->count);
+  if (a->m < 0 || a->k < 0) return fail(LSFA_ERR_INVALID, "negative size (m=%d k=%d)", a->m, a->k);
+  if (a->m > 8) return fail(LSFA_ERR_UNSUPPORTED, "gemv takes at most 8 rows (m=%d)", a->m);
+  for (int i = 0; i < a->count; ++i) {
+    if (a->n[i] < 0) return fail(LSFA_ERR_INVALID, "negative size (n=%d)", a->n[i]);
+    if (a->n[i] % 8 != 0) return fail(LSFA_ERR_UNSUPPORTED, "gemv needs n %% 8 == 0 (n=%d)", a->n[i]);
+  }
+  const long long N = gemv_total_n(a);
+  if (N > (long long)LSFA_GEMV_COUNTER_BYTES / 64 * 256)
+    return fail(LSFA_ERR_UNSUPPORTED, "gemv takes at most %d columns (n=%lld)", LSFA_GEMV_COUNTER_BYTES / 64 * 256, N);
+  if (a->m == 0 || N == 0) return ok();
+  if (!a->x) return fail(LSFA_ERR_INVALID, "x, w and y must be non-NULL");
+  if (a->x_stride < a->k) return fail(LSFA_ERR_INVALID, "x_stride must be >= k");
+  for (int i = 0; i < a->count; ++i) {
+    if (a->n[i] == 0) continue;
+    if (!a->w[i] || !a->y[i]) return fail(LSFA_ERR_INVALID, "x, w and y must be non-NULL");
+    if (a->w_stride[i] < a->n[i] || a->w_stride[i] % 8 != 0 || !aligned16(a->w[i]))
+      return fail(LSFA_ERR_UNSUPPORTED, "w rows must be 16-byte aligned with w_stride >= n and a multiple of 8");
+    if (a->y_stride[i] < a->n[i]) return fail(LSFA_ERR_INVALID, "y_stride must be >= n");
+  }
+  const GemvSplit g = gemv_split(a->m, a->k, N);
+  if (g.splits > 65535) return fail(LSFA_ERR_UNSUPPORTED, "k too large for one launch");
+  if (g.bytes > 0) {
+    if (!a->workspace) return fail(LSFA_ERR_INVALID, "workspace must be non-NULL");
+    if (a->workspace_bytes < g.bytes)
+      return fail(LSFA_ERR_INVALID, "workspace_bytes %llu is below the %llu bytes lsfa_gemv_workspace_size asks for",
+                  (unsigned long long)a->workspace_bytes, (unsigned long long)g.bytes);
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
+      return fail(LSFA_ERR_INVALID, "workspace is not 256-byte aligned");
+  }
+  return ok();
+}
+
+int lsfa_gemv_group_workspace_size(const lsfa_gemv_group_args* a, uint64_t* bytes) {
+  if (a == nullptr || bytes == nullptr) return fail(LSFA_ERR_INVALID, "args or bytes is NULL");
+  *bytes = gemv_split(a->m, a->k, gemv_total_n(a)).bytes;
+  return ok();
+}
+
+int lsfa_gemv_group(const lsfa_gemv_group_args* a, void* stream) {
+  int rc = lsfa_gemv_group_check(a);
+  if (rc) return rc;
+  const long long N = gemv_total_n(a);
+  if (a->m == 0 || N == 0) return ok();
+  const GemvSplit g = gemv_split(a->m, a->k, N);
+  lsfa::GemvParams p;
+  memset(&p, 0, sizeof(p));
+  p.x = a->x;
+  int off = 0;
+  for (int i = 0; i < 4; ++i) {
+    p.col_off[i] = off;
+    if (i < a->count) {
+      p.w[i] = a->w[i]; p.y[i] = a->y[i]; p.sw[i] = a->w_stride[i]; p.sy[i] = a->y_stride[i];
+      off += a->n[i];
+    }
+  }
+  p.col_off[4] = off;
+  for (int i = a->count; i < 4; ++i) p.col_off[i] = off;  // unused matrices own no column
+  p.groups = a->count;
+  if (g.splits > 1) {
+    p.counters = static_cast<int*>(a->workspace);
+    p.partial = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + g.counter_bytes);
+  }
+  p.sx = a->x_stride;
+  p.M = a->m; p.K = a->k; p.N = (int)N;
+  p.kc = g.kc; p.splits = g.splits;
+  hipError_t e = lsfa::gemv(p, a->dtype == LSFA_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "gemv launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int lsfa_gemv_check(const lsfa_gemv_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  const lsfa_gemv_group_args gr = gemv_as_group(a);
+  return lsfa_gemv_group_check(&gr);
+}
+
+int lsfa_gemv_workspace_size(const lsfa_gemv_args* a, uint64_t* bytes) {
+  if (a == nullptr || bytes == nullptr) return fail(LSFA_ERR_INVALID, "args or bytes is NULL");
+  const lsfa_gemv_group_args gr = gemv_as_group(a);
+  return lsfa_gemv_group_workspace_size(&gr, bytes);
+}
+
+int lsfa_gemv(const lsfa_gemv_args* a, void* stream) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  const lsfa_gemv_group_args gr = gemv_as_group(a);
+  return lsfa_gemv_group(&gr, stream);
 }
 
 int lsfa_rope_check(const lsfa_rope_args* a) {

@@ -187,6 +187,25 @@ struct BwdParams {
 // Paged-KV decode (one query token per sequence); strides in elements.
 constexpr int kDecodeMaxTableSlots = 512;  // block-table entries one split may span
 
+// Skinny GEMM y[M, N] = x[M, K] @ W[K, N] (M <= 8; element strides; W rows
+// contiguous). partial: fp32 workspace [splits][M][N].
+struct GemvParams {
+  // Up to four weight matrices sharing x and K; their columns are numbered
+  // one after another (matrix g holds columns col_off[g] .. col_off[g+1]-1 of
+  // a virtual y of N = col_off[groups] columns).
+  const void* x;
+  const void* w[4];
+  void* y[4];
+  int64_t sw[4], sy[4];
+  int col_off[5];
+  int groups;
+  float* partial;  // [splits][M][N] fp32 (splits > 1)
+  int* counters;   // 16 per 256-column block, zero on entry and on exit (splits > 1)
+  int64_t sx;
+  int M, K, N;
+  int kc, splits;  // K-range per split and the number of splits
+};
+
 // Which decode kernel serves a group size Hq/Hkv and block size 2^shift: the
 // lane-group kernel for groups 1, 2, 4, 8; the MFMA kernel for other groups
 // (up to 32) with blocks of at least 16 tokens.

@@ -1,0 +1,266 @@
+// Skinny GEMM (M <= 8 rows) for decode-time projections: y[M, N] = x[M, K] @ W[K, N]
+// with W in the [in, out] row-major layout the model stores
+// (model/minimal_llama.py's weights), bf16/fp16 in, fp32 accumulate. Up to
+// four matrices that share x (a decoder's q/k/v or gate/up projections) run
+// as one launch over their concatenated columns.
+//
+// At M <= 8 the product is a pass over W (about M FLOP per weight byte), so it
+// is HBM-bound: the kernel is built to stream W once at full rate, in one
+// launch.
+//   Grid (ceil(N / 256), splits). A workgroup owns 256 columns and one K-range
+//   of kc rows; thread (cg, kg) = (tid % 32, tid / 32) reads 16 bytes
+//   (8 columns) of rows kg, kg + 8, ... of the range, eight rows in flight, so
+//   each wave-load covers two 512-byte row segments, and keeps M x 8 fp32
+//   sums. x's K-range sits in LDS as fp32. The 8 K-groups are summed through
+//   LDS.
+//   With one split the workgroup rounds its sums into y. Otherwise it stores
+//   them as an fp32 partial block [split][M][256 columns] and counts its
+//   arrival in two levels: split s adds one to sub-counter s % 8 of its column
+//   block, and the last arrival of each sub-group adds one to the block's main
+//   counter. Atomics on one address serialise at about 175 ns each on MI355X,
+//   so one counter for 64 splits costs 11 us; two levels cost at most 8 + 8.
+//   The workgroup that arrives last at the main counter sums the splits'
+//   partials, rounds once into y, and every counter is put back to zero by the
+//   workgroup that completed it, so all are zero again when the launch ends.
+//   Deterministic: the order of the sum does not depend on which workgroup
+//   arrives last. No memsets: graph-capturable.
+//   Hand-over without cache maintenance: the partials are written and read
+//   with device-scope atomic stores and loads (coherent across the XCDs' L2s
+//   without a writeback or an invalidate) and every store has completed
+//   (s_waitcnt vmcnt(0)) before the workgroup's barrier and its counter add.
+//   That is the compiler's own release sequence for device scope minus the L2
+//   writeback (buffer_wbl2), which only non-atomic stores need; a release
+//   fence would write the L2 back once per workgroup, about 10x the time of
+//   the whole pass.
+#include "fa_common.hpp"
+
+namespace lsfa {
+
+constexpr int kGemvCols = 256;  // columns per workgroup (32 groups of 8)
+constexpr int kGemvKG = 8;      // K-groups per workgroup
+constexpr int kGemvCounterSlots = 16;  // per column block: 8 sub-counters, the main counter, padding
+typedef uint64_t u64x2x2[4];    // 8 fp32 partials as four 8-byte words
+
+// Matrix of virtual column n (uniform selects, no indexing of the kernel
+// arguments by a lane value).
+__device__ __forceinline__ int gemv_group(const GemvParams& p, int n) {
+  return (n >= p.col_off[1]) + (n >= p.col_off[2]) + (n >= p.col_off[3]);
+}
+template <typename V>
+__device__ __forceinline__ V gemv_pick(int g, V a0, V a1, V a2, V a3) {
+  return g == 0 ? a0 : (g == 1 ? a1 : (g == 2 ? a2 : a3));
+}
+template <typename T>
+__device__ __forceinline__ T* gemv_out(const GemvParams& p, int n, int m) {
+  const int g = gemv_group(p, n);
+  T* y = (T*)gemv_pick(g, p.y[0], p.y[1], p.y[2], p.y[3]);
+  const int64_t sy = gemv_pick(g, p.sy[0], p.sy[1], p.sy[2], p.sy[3]);
+  const int col_off = gemv_pick(g, p.col_off[0], p.col_off[1], p.col_off[2], p.col_off[3]);
+  return y + (int64_t)m * sy + (n - col_off);
+}
+
+// M is the compile-time row capacity (1, 2, 4 or 8); p.M <= M rows are real.
+// Rows past p.M have x = 0 in LDS and their sums are not stored.
+template <typename T, int M>
+__global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
+  extern __shared__ float gemv_smem[];  // x chunk [M][kc], then the K-group sums
+  __shared__ int last_arrival;
+  const int tid = threadIdx.x;
+  const int cg = tid & 31, kg = tid >> 5;
+  const int n0 = blockIdx.x * kGemvCols + cg * 8;
+  const int split = blockIdx.y;
+  const int k_begin = split * p.kc;
+  const int k_len = max(0, min(p.K, k_begin + p.kc) - k_begin);
+  float* xs = gemv_smem;
+  for (int idx = tid; idx < M * k_len; idx += 256) {
+    const int m = idx / k_len, k = idx - m * k_len;
+    xs[m * p.kc + k] = m < p.M ? (float)((const T*)p.x)[(int64_t)m * p.sx + k_begin + k] : 0.f;
+  }
+  __syncthreads();
+
+  float acc[M][8];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[m][e] = 0.f;
+
+  auto fma_row = [&](const u32x4 raw, int k) {
+    const typename VecT<T>::x8 wv = __builtin_bit_cast(typename VecT<T>::x8, raw);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float xv = xs[m * p.kc + k];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(xv, (float)wv[e], acc[m][e]);
+    }
+  };
+
+  if (n0 < p.N) {
+    const int g = gemv_group(p, n0);
+    const int64_t sw = gemv_pick(g, p.sw[0], p.sw[1], p.sw[2], p.sw[3]);
+    const T* wp = (const T*)gemv_pick(g, p.w[0], p.w[1], p.w[2], p.w[3]) + (int64_t)(k_begin + kg) * sw +
+                  (n0 - gemv_pick(g, p.col_off[0], p.col_off[1], p.col_off[2], p.col_off[3]));
+    const int64_t step = (int64_t)kGemvKG * sw;
+    int k = kg;
+    for (; k + 7 * kGemvKG < k_len; k += 8 * kGemvKG) {  // eight rows in flight
+      u32x4 raw[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) raw[u] = __builtin_nontemporal_load((const u32x4*)(wp + u * step));
+      __builtin_amdgcn_sched_barrier(0);  // all eight loads issue before the first use
+      wp += 8 * step;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) fma_row(raw[u], k + u * kGemvKG);
+    }
+    if (k + 3 * kGemvKG < k_len) {
+      u32x4 raw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) raw[u] = __builtin_nontemporal_load((const u32x4*)(wp + u * step));
+      __builtin_amdgcn_sched_barrier(0);
+      wp += 4 * step;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) fma_row(raw[u], k + u * kGemvKG);
+      k += 4 * kGemvKG;
+    }
+    for (; k < k_len; k += kGemvKG) {
+      fma_row(__builtin_nontemporal_load((const u32x4*)wp), k);
+      wp += step;
+    }
+  }
+
+  // Sum the K-groups: red[kg][m][column] over the x chunk.
+  __syncthreads();  // every thread is done with xs
+  float* red = gemv_smem;
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[(kg * M + m) * kGemvCols + cg * 8 + e] = acc[m][e];
+  __syncthreads();
+  const int n = blockIdx.x * kGemvCols + tid;
+  const bool col_ok = n < p.N;
+  float sum[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    sum[m] = 0.f;
+#pragma unroll
+    for (int g = 0; g < kGemvKG; ++g) sum[m] += red[(g * M + m) * kGemvCols + tid];
+  }
+
+  if (p.splits == 1) {
+    if (col_ok) {
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+        if (m < p.M) *gemv_out<T>(p, n, m) = (T)sum[m];
+    }
+    return;
+  }
+
+  if (col_ok) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (m < p.M)
+        __hip_atomic_store(p.partial + ((int64_t)split * p.M + m) * p.N + n, sum[m], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partials have reached device scope
+  __syncthreads();
+  if (tid == 0) {
+    int* ctr = p.counters + blockIdx.x * kGemvCounterSlots;
+    const int group = split & 7;
+    const int group_size = (p.splits - group + 7) >> 3;
+    const int groups = min(p.splits, 8);
+    bool last = false;
+    if (__hip_atomic_fetch_add(ctr + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == group_size - 1) {
+      __hip_atomic_store(ctr + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = __hip_atomic_fetch_add(ctr + 8, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1;
+      if (last) __hip_atomic_store(ctr + 8, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    last_arrival = last;
+  }
+  __syncthreads();
+  if (!last_arrival) return;
+  // The last workgroup sums the splits with the same (cg, kg) split of the
+  // work as the pass: thread (cg, kg) adds 8 columns of splits kg, kg + 8, ...
+  // (independent 8-byte loads, many in flight), then the K-groups are added
+  // through LDS in a fixed order.
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[m][e] = 0.f;
+  if (n0 < p.N) {
+    const int64_t sstride = (int64_t)p.M * p.N;
+    constexpr int SB = M >= 8 ? 1 : 8 / M;  // splits per batch: 32 loads in flight
+    for (int s0 = kg; s0 < p.splits; s0 += SB * kGemvKG) {
+      u64x2x2 v[SB][M];
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        const int s2 = s0 + b * kGemvKG;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          uint64_t* src = (uint64_t*)(p.partial + s2 * sstride + (int64_t)m * p.N + n0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            v[b][m][q] = (s2 < p.splits && m < p.M)
+                             ? __hip_atomic_load(src + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < SB; ++b)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[m][2 * q] += __uint_as_float((uint32_t)v[b][m][q]);
+            acc[m][2 * q + 1] += __uint_as_float((uint32_t)(v[b][m][q] >> 32));
+          }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[(kg * M + m) * kGemvCols + cg * 8 + e] = acc[m][e];
+  __syncthreads();
+  if (col_ok) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if (m < p.M) {
+        float t = 0.f;
+#pragma unroll
+        for (int g = 0; g < kGemvKG; ++g) t += red[(g * M + m) * kGemvCols + tid];
+        *gemv_out<T>(p, n, m) = (T)t;
+      }
+    }
+  }
+}
+
+template <typename T, int M>
+static hipError_t launch_gemv_m(const GemvParams& p, hipStream_t s) {
+  const size_t xs_bytes = (size_t)M * p.kc * 4;
+  const size_t red_bytes = (size_t)kGemvKG * M * kGemvCols * 4;
+  const size_t lds = xs_bytes > red_bytes ? xs_bytes : red_bytes;
+  const dim3 grid((unsigned)((p.N + kGemvCols - 1) / kGemvCols), (unsigned)p.splits);
+  hipLaunchKernelGGL((fa_gemv_kernel<T, M>), grid, dim3(256), lds, s, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_gemv(const GemvParams& p, hipStream_t s) {
+  switch (p.M) {
+    case 1: return launch_gemv_m<T, 1>(p, s);
+    case 2: return launch_gemv_m<T, 2>(p, s);
+    case 3:
+    case 4: return launch_gemv_m<T, 4>(p, s);
+    default: return launch_gemv_m<T, 8>(p, s);
+  }
+}
+
+// Row capacity of the kernel that serves m rows (3 and 5..7 run the next one up).
+int gemv_capacity(int m) { return m <= 2 ? m : (m <= 4 ? 4 : 8); }
+
+// Host entry used by the C ABI layer (arguments validated, the split chosen
+// so that kc * capacity * 4 bytes of x fit in 32 KB of LDS).
+hipError_t gemv(const GemvParams& p, bool is_bf16, hipStream_t s) {
+  if (p.M == 0 || p.N == 0) return hipSuccess;
+  return is_bf16 ? launch_gemv<__bf16>(p, s) : launch_gemv<_Float16>(p, s);
+}
+
+}  // namespace lsfa

@@ -7,8 +7,107 @@ argument checks and AssertionErrors (kernels/tiled_matmul.py:135-140) so the
 model code and the reference's tests call it unchanged. fp32 operands use
 IEEE fp32 (torch's default, allow_tf32 off), as the reference's
 input_precision="ieee" does.
+
+Decode-time calls carry 1..8 rows (one per sequence in the batch). There a
+GEMM is a single pass over B's bytes, so bf16/fp16 products with M <= 8 go to
+the library's skinny kernel (lsfa_gemv: one launch, a K-split pass over B at
+HBM rate whose last workgroup per column block sums the fp32 partials and
+rounds once), which hipBLASLt's general tiles reach at a fraction of the
+bandwidth.
+
+Projections that share their input (a decoder's q/k/v, gate/up) go through
+matmul_shared_input, which runs them as one lsfa_gemv_group launch over their
+concatenated columns when they qualify for the skinny kernel.
+
+lsfa_gemv's workspace carries arrival counters that must start at zero and
+that every call leaves at zero, so this module keeps one zero-initialised
+workspace per (device, stream) and reuses it for every call on that stream
+(stream order keeps the calls apart). A workspace that grows is replaced, not
+freed: a captured HIP graph that recorded the old one keeps using it.
 """
 import torch
+
+from .. import _lib
+
+SKINNY_MAX_ROWS = 8
+
+_workspaces = {}  # (device index, stream handle) -> every workspace created for it, the last in use
+
+
+def _workspace(device, stream, nbytes):
+    bufs = _workspaces.setdefault((device.index, stream), [])
+    if not bufs or bufs[-1].numel() < nbytes:
+        bufs.append(torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device))
+    return bufs[-1]
+
+
+def _skinny_ok(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return (a.shape[0] <= SKINNY_MAX_ROWS and a.dtype in (torch.bfloat16, torch.float16)
+            and a.stride(1) == 1 and b.stride(1) == 1 and b.shape[1] % 8 == 0
+            and b.stride(0) % 8 == 0 and b.stride(0) >= b.shape[1] and b.data_ptr() % 16 == 0)
+
+
+def skinny_matmul(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+    """C = A @ B for a [M <= 8, K], b [K, N] (bf16/fp16, N % 8 == 0, rows of
+    b 16-byte aligned) through lsfa_gemv; fp32 accumulation, one rounding."""
+    assert _skinny_ok(a, b), "skinny_matmul needs M <= 8, bf16/fp16, unit column strides, N % 8 == 0"
+    M, K = a.shape
+    N = b.shape[1]
+    if out is None:
+        out = torch.empty(M, N, dtype=a.dtype, device=a.device)
+    if M == 0 or N == 0:
+        return out
+    if K == 0:
+        return out.zero_()
+    args = _lib.GemvArgs(x=a.data_ptr(), w=b.data_ptr(), y=out.data_ptr(), workspace=None, workspace_bytes=0,
+                         x_stride=a.stride(0), w_stride=b.stride(0), y_stride=out.stride(0),
+                         dtype=_lib.TORCH_TO_LSFA[a.dtype], m=M, k=K, n=N)
+    nbytes = _lib.gemv_workspace_size(args)
+    with torch.cuda.device(a.device):
+        stream = _lib.current_stream(a.device)
+        if nbytes:
+            ws = _workspace(a.device, stream, nbytes)
+            args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+        _lib.gemv(args, stream)
+    return out
+
+
+def skinny_matmul_group(a: torch.Tensor, bs, outs=None):
+    """[a @ b for b in bs] for up to four b sharing a (each as for
+    skinny_matmul) in one lsfa_gemv_group launch."""
+    assert 1 <= len(bs) <= _lib.GEMV_MAX_GROUP, f"1..{_lib.GEMV_MAX_GROUP} matrices per group"
+    assert all(_skinny_ok(a, b) and b.shape[0] == a.shape[1] and b.dtype == a.dtype for b in bs), (
+        "every matrix must qualify for skinny_matmul with the shared input")
+    M, K = a.shape
+    if outs is None:
+        outs = [torch.empty(M, b.shape[1], dtype=a.dtype, device=a.device) for b in bs]
+    if M == 0 or sum(b.shape[1] for b in bs) == 0:
+        return outs
+    if K == 0:
+        return [o.zero_() for o in outs]
+    args = _lib.GemvGroupArgs(x=a.data_ptr(), x_stride=a.stride(0), dtype=_lib.TORCH_TO_LSFA[a.dtype], m=M, k=K,
+                              count=len(bs))
+    for i, (b, o) in enumerate(zip(bs, outs)):
+        args.w[i], args.y[i] = b.data_ptr(), o.data_ptr()
+        args.w_stride[i], args.y_stride[i], args.n[i] = b.stride(0), o.stride(0), b.shape[1]
+    nbytes = _lib.gemv_group_workspace_size(args)
+    with torch.cuda.device(a.device):
+        stream = _lib.current_stream(a.device)
+        if nbytes:
+            ws = _workspace(a.device, stream, nbytes)
+            args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+        _lib.gemv_group(args, stream)
+    return outs
+
+
+def matmul_shared_input(a: torch.Tensor, bs):
+    """[matmul(a, b) for b in bs]: one grouped skinny launch when every
+    product qualifies for the skinny kernel, else one matmul each."""
+    if len(bs) <= _lib.GEMV_MAX_GROUP and a.ndim == 2 and a.is_cuda and all(
+            b.ndim == 2 and b.is_cuda and b.dtype == a.dtype and b.shape[0] == a.shape[1] and _skinny_ok(a, b)
+            for b in bs):
+        return skinny_matmul_group(a, bs)
+    return [matmul(a, b) for b in bs]
 
 
 def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -17,4 +116,6 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     assert a.shape[1] == b.shape[0], f"inner dims must match: a is {tuple(a.shape)}, b is {tuple(b.shape)}"
     assert a.is_cuda and b.is_cuda, "the gfx950 path needs GPU tensors"
     assert a.dtype == b.dtype, f"dtype mismatch: a={a.dtype} b={b.dtype}"
+    if _skinny_ok(a, b):
+        return skinny_matmul(a, b)
     return torch.matmul(a, b)

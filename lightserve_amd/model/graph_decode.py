@@ -32,6 +32,7 @@ import torch.nn.functional as F
 from ..kernels.paged_attention import paged_attention_decode, paged_prefill
 from ..kernels.rope import apply_rope_
 from ..kernels.fused_rmsnorm_residual import fused_add_rmsnorm
+from ..kernels.tiled_matmul import matmul, matmul_shared_input
 from .minimal_llama import add_norm, init_weights, llama3_8b_shape, llama_forward, precompute_rope
 
 SEED_TOKEN_ID = 1
@@ -144,20 +145,18 @@ class KVCacheDecoder:
         pending = None
         for i, layer in enumerate(self.w.layers):
             h, residual = add_norm(pending, residual, layer.input_layernorm_weight, cfg.rms_eps)
-            q = torch.matmul(h, layer.q_proj)
-            k = torch.matmul(h, layer.k_proj)
-            v = torch.matmul(h, layer.v_proj)
+            q, k, v = matmul_shared_input(h, (layer.q_proj, layer.k_proj, layer.v_proj))
             apply_rope_(q.view(B, nh, 1, hd), k.view(B, nkv, 1, hd), self.cos, self.sin, positions=pos)
             self.k_cache[i].view(-1, nkv, hd).index_copy_(0, slot, k.view(B, nkv, hd))
             self.v_cache[i].view(-1, nkv, hd).index_copy_(0, slot, v.view(B, nkv, hd))
             o = paged_attention_decode(q.view(B, nh, hd), self.k_cache[i], self.v_cache[i], self.block_tables,
                                        lens, max_seq_len=cfg.max_seq_len)
-            h2, residual = fused_add_rmsnorm(torch.matmul(o.view(B, nh * hd), layer.o_proj), residual,
+            h2, residual = fused_add_rmsnorm(matmul(o.view(B, nh * hd), layer.o_proj), residual,
                                              layer.post_attention_layernorm_weight, cfg.rms_eps)
-            mlp = F.silu(torch.matmul(h2, layer.gate_proj)) * torch.matmul(h2, layer.up_proj)
-            pending = torch.matmul(mlp, layer.down_proj)
+            gate, up = matmul_shared_input(h2, (layer.gate_proj, layer.up_proj))
+            pending = matmul(F.silu(gate) * up, layer.down_proj)
         final, _ = add_norm(pending, residual, self.w.norm_weight, cfg.rms_eps)
-        return torch.matmul(final, self.w.lm_head)
+        return matmul(final, self.w.lm_head)
 
     def prefill(self, prompt, chunk_size):
         """Caches a prompt [B, P] chunk by chunk (the engine's chunked prefill:
@@ -182,23 +181,23 @@ class KVCacheDecoder:
             pending = None
             for i, layer in enumerate(self.w.layers):
                 h, residual = add_norm(pending, residual, layer.input_layernorm_weight, cfg.rms_eps)
-                q = torch.matmul(h, layer.q_proj)
-                k = torch.matmul(h, layer.k_proj)
-                v = torch.matmul(h, layer.v_proj)
+                q = matmul(h, layer.q_proj)
+                k = matmul(h, layer.k_proj)
+                v = matmul(h, layer.v_proj)
                 apply_rope_(q.view(B, c, nh, hd).transpose(1, 2), k.view(B, c, nkv, hd).transpose(1, 2),
                             self.cos, self.sin, positions=pos)
                 self.k_cache[i].view(-1, nkv, hd).index_copy_(0, slot, k.view(B * c, nkv, hd))
                 self.v_cache[i].view(-1, nkv, hd).index_copy_(0, slot, v.view(B * c, nkv, hd))
                 o = paged_prefill(q.view(B * c, nh, hd), self.k_cache[i], self.v_cache[i], self.block_tables, cu, lens,
                                   max_seqlen_q=c)
-                h2, residual = fused_add_rmsnorm(torch.matmul(o.view(B * c, nh * hd), layer.o_proj), residual,
+                h2, residual = fused_add_rmsnorm(matmul(o.view(B * c, nh * hd), layer.o_proj), residual,
                                                  layer.post_attention_layernorm_weight, cfg.rms_eps)
-                mlp = F.silu(torch.matmul(h2, layer.gate_proj)) * torch.matmul(h2, layer.up_proj)
-                pending = torch.matmul(mlp, layer.down_proj)
+                mlp = F.silu(matmul(h2, layer.gate_proj)) * matmul(h2, layer.up_proj)
+                pending = matmul(mlp, layer.down_proj)
             last = slice(c - 1, B * c, c)  # each sequence's last token of the chunk
             final, _ = add_norm(pending[last].contiguous() if pending is not None else None,
                                 residual[last].contiguous(), self.w.norm_weight, cfg.rms_eps)
-            logits = torch.matmul(final, self.w.lm_head)
+            logits = matmul(final, self.w.lm_head)
             self.seq_lens.add_(c)
         self.tokens.copy_(logits.argmax(dim=-1))
         return logits

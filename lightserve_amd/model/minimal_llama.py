@@ -16,9 +16,10 @@ model/cuda_graph_decode.py run against this module unchanged. What differs:
     its fused kernel (:197-238): a sublayer's output is folded into the
     residual by the next norm. The first norm has no pending output and is
     the same kernel without the add (the reference adds a zero tensor).
-  - Linear layers are torch matmuls (hipBLASLt) on the reference's [in, out]
-    weights: kernels.tiled_matmul.matmul is the same call behind the
-    reference's argument checks, which the model skips.
+  - Linear layers go through kernels.tiled_matmul.matmul on the reference's
+    [in, out] weights, as the reference's do through its tiled GEMM: hipBLASLt
+    for prefill-sized products, the library's skinny kernel (lsfa_gemv) for
+    products of at most 8 rows (decode steps).
 The forward needs no host synchronisation, so it can be captured in a HIP
 graph (model/graph_decode.py).
 """
@@ -33,6 +34,7 @@ from ..kernels.fused_rmsnorm_residual import fused_add_rmsnorm
 from ..kernels.fused_rmsnorm_residual import rmsnorm as rmsnorm_kernel
 from ..kernels.flash_attention_varlen import flash_attention_varlen_forward
 from ..kernels.rope import apply_rope_
+from ..kernels.tiled_matmul import matmul
 
 
 @dataclass
@@ -150,9 +152,9 @@ def add_norm(x, residual, weight, eps):
 def attention_block(layer, config, normed_2d, B, N, cos, sin, causal, positions=None):
     """q/k/v projections, in-place RoPE, attention; returns [B*N, n_heads*head_dim]."""
     nh, nkv, hd = config.n_heads, config.kv_heads, config.head_dim
-    q = torch.matmul(normed_2d, layer.q_proj)   # [B*N, nh*hd]
-    k = torch.matmul(normed_2d, layer.k_proj)   # [B*N, nkv*hd]
-    v = torch.matmul(normed_2d, layer.v_proj)
+    q = matmul(normed_2d, layer.q_proj)   # [B*N, nh*hd]
+    k = matmul(normed_2d, layer.k_proj)   # [B*N, nkv*hd]
+    v = matmul(normed_2d, layer.v_proj)
     q4 = q.view(B, N, nh, hd).transpose(1, 2)   # [B, nh, N, hd] views, no copies
     k4 = k.view(B, N, nkv, hd).transpose(1, 2)
     apply_rope_(q4, k4, cos, sin, positions)
@@ -177,9 +179,9 @@ def llama_forward(weights: LlamaWeights, config: LlamaConfig, input_ids: torch.T
     for layer in weights.layers:
         normed, residual = add_norm(pending, residual, layer.input_layernorm_weight, config.rms_eps)
         attn = attention_block(layer, config, normed, B, N, cos, sin, causal)
-        normed2, residual = fused_add_rmsnorm(torch.matmul(attn, layer.o_proj), residual,
+        normed2, residual = fused_add_rmsnorm(matmul(attn, layer.o_proj), residual,
                                               layer.post_attention_layernorm_weight, config.rms_eps)
-        mlp = F.silu(torch.matmul(normed2, layer.gate_proj)) * torch.matmul(normed2, layer.up_proj)
-        pending = torch.matmul(mlp, layer.down_proj)
+        mlp = F.silu(matmul(normed2, layer.gate_proj)) * matmul(normed2, layer.up_proj)
+        pending = matmul(mlp, layer.down_proj)
     final, _ = add_norm(pending, residual, weights.norm_weight, config.rms_eps)
-    return torch.matmul(final, weights.lm_head).reshape(B, N, config.vocab_size)
+    return matmul(final, weights.lm_head).reshape(B, N, config.vocab_size)

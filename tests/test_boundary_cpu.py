@@ -114,7 +114,10 @@ def test_struct_layout_matches_header(built_library):
            ' offsetof(lsfa_rmsnorm_args, dtype), offsetof(lsfa_rmsnorm_args, eps));'
            ' printf("%zu %zu %zu %zu\\n", sizeof(lsfa_prefill_paged_args),'
            ' offsetof(lsfa_prefill_paged_args, block_table_stride), offsetof(lsfa_prefill_paged_args, causal),'
-           ' offsetof(lsfa_prefill_paged_args, sm_scale)); return 0;}\n')
+           ' offsetof(lsfa_prefill_paged_args, sm_scale)); printf("%zu %zu %zu\\n", sizeof(lsfa_gemv_args),'
+           ' offsetof(lsfa_gemv_args, dtype), offsetof(lsfa_gemv_args, n));'
+           ' printf("%zu %zu %zu %zu\\n", sizeof(lsfa_gemv_group_args), offsetof(lsfa_gemv_group_args, y_stride),'
+           ' offsetof(lsfa_gemv_group_args, n), offsetof(lsfa_gemv_group_args, count)); return 0;}\n')
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "t.c")
         exe = os.path.join(d, "t")
@@ -127,7 +130,10 @@ def test_struct_layout_matches_header(built_library):
                      ctypes.sizeof(_lib.RopeArgs), _lib.RopeArgs.table_stride.offset, _lib.RopeArgs.max_pos.offset,
                      ctypes.sizeof(_lib.RmsNormArgs), _lib.RmsNormArgs.dtype.offset, _lib.RmsNormArgs.eps.offset,
                      ctypes.sizeof(_lib.PrefillPagedArgs), _lib.PrefillPagedArgs.block_table_stride.offset,
-                     _lib.PrefillPagedArgs.causal.offset, _lib.PrefillPagedArgs.sm_scale.offset]
+                     _lib.PrefillPagedArgs.causal.offset, _lib.PrefillPagedArgs.sm_scale.offset,
+                     ctypes.sizeof(_lib.GemvArgs), _lib.GemvArgs.dtype.offset, _lib.GemvArgs.n.offset,
+                     ctypes.sizeof(_lib.GemvGroupArgs), _lib.GemvGroupArgs.y_stride.offset,
+                     _lib.GemvGroupArgs.n.offset, _lib.GemvGroupArgs.count.offset]
 
 
 def _fwd_args(**kw):
@@ -361,6 +367,92 @@ def test_abi_rmsnorm_validation(built_library):
     _lib.rmsnorm(_norm_args(rows=0, x=None, out=None), 0)  # empty: no-op
     with pytest.raises(RuntimeError, match="LSFA_ERR_INVALID"):
         _lib.rmsnorm(_norm_args(rows=-1), 0)
+
+
+def _gemv_args(**kw):
+    base = dict(x=4096, w=8192, y=12288, workspace=1 << 20, workspace_bytes=1 << 30, x_stride=4096,
+                w_stride=4096, y_stride=4096, dtype=_lib.DTYPE_BF16, m=4, k=4096, n=4096)
+    base.update(kw)
+    return _lib.GemvArgs(**base)
+
+
+def test_abi_gemv_validation(built_library):
+    """Host-only validation and workspace sizing of lsfa_gemv (fake pointers)."""
+    assert _lib.gemv_check(_gemv_args())[0] == 0
+    for m in range(1, 9):
+        assert _lib.gemv_check(_gemv_args(m=m))[0] == 0
+    rc, msg = _lib.gemv_check(_gemv_args(m=9))
+    assert rc == -2 and "8 rows" in msg
+    rc, msg = _lib.gemv_check(_gemv_args(n=4092, w_stride=4096))
+    assert rc == -2 and "n % 8" in msg
+    rc, msg = _lib.gemv_check(_gemv_args(w=8194))
+    assert rc == -2 and "aligned" in msg
+    rc, msg = _lib.gemv_check(_gemv_args(w_stride=4100))
+    assert rc == -2
+    rc, msg = _lib.gemv_check(_gemv_args(dtype=_lib.DTYPE_FP32))
+    assert rc == -2 and "bf16" in msg
+    rc, msg = _lib.gemv_check(_gemv_args(x_stride=100))
+    assert rc == -1 and "x_stride" in msg
+    rc, msg = _lib.gemv_check(_gemv_args(workspace=1 << 20 | 64))
+    assert rc == -1 and "aligned" in msg
+    need = _lib.gemv_workspace_size(_gemv_args())
+    assert need % 256 == 0 and need >= 4 * 4096 * 4  # at least one fp32 partial row block per row
+    rc, msg = _lib.gemv_check(_gemv_args(workspace_bytes=need - 256))
+    assert rc == -1 and "workspace_bytes" in msg
+    assert _lib.gemv_check(_gemv_args(workspace_bytes=need))[0] == 0
+    # the split keeps K-ranges within 64..2048 rows and about 1024 workgroups;
+    # layout: a fixed 256 KB of counters, then [splits][m][n] fp32
+    for k, n in [(4096, 4096), (14336, 4096), (4096, 128256), (100000, 1024)]:
+        col_blocks = (n + 255) // 256
+        splits = (_lib.gemv_workspace_size(_gemv_args(m=1, k=k, n=n)) - 262144) // 4 // n
+        assert 2 <= splits <= max(-(-1024 // col_blocks), (k + 2047) // 2048), (k, n, splits)
+    assert _lib.gemv_workspace_size(_gemv_args(m=1, k=64, n=64)) == 0  # one split: no workspace
+    assert _lib.gemv_check(_gemv_args(m=1, k=64, n=64, workspace=None, workspace_bytes=0))[0] == 0
+    rc, msg = _lib.gemv_check(_gemv_args(n=1048576 + 8, w_stride=1048576 + 8))
+    assert rc == -2 and "columns" in msg
+    _lib.gemv(_gemv_args(m=0, x=None, y=None), 0)  # empty: no-op, no GPU touched
+    with pytest.raises(RuntimeError, match="8 rows"):
+        _lib.gemv(_gemv_args(m=9), 0)
+
+
+def _group_args(ns, **kw):
+    a = _lib.GemvGroupArgs(x=4096, workspace=1 << 20, workspace_bytes=1 << 30, x_stride=4096,
+                           dtype=_lib.DTYPE_BF16, m=2, k=4096, count=len(ns))
+    for i, n in enumerate(ns):
+        a.w[i], a.y[i] = (1 << 24) * (i + 1), (1 << 28) + (1 << 20) * i
+        a.w_stride[i], a.y_stride[i], a.n[i] = n, n, n
+    for key, value in kw.items():
+        setattr(a, key, value)
+    return a
+
+
+def test_abi_gemv_group_validation(built_library):
+    """The grouped skinny GEMM: validation per matrix, workspace sized for
+    the concatenated columns (the same as one matrix of that width)."""
+    ns = [4096, 1024, 1024]
+    assert _lib.gemv_group_check(_group_args(ns))[0] == 0
+    assert _lib.gemv_group_workspace_size(_group_args(ns)) == _lib.gemv_workspace_size(
+        _gemv_args(m=2, k=4096, n=sum(ns)))
+    rc, msg = _lib.gemv_group_check(_group_args(ns, count=5))
+    assert rc == -1 and "count" in msg
+    rc, msg = _lib.gemv_group_check(_group_args(ns, count=0))
+    assert rc == -1 and "count" in msg
+    bad = _group_args(ns)
+    bad.n[1] = 1020
+    assert _lib.gemv_group_check(bad)[0] == -2
+    bad = _group_args(ns)
+    bad.w[2] = (1 << 24) + 8
+    rc, msg = _lib.gemv_group_check(bad)
+    assert rc == -2 and "aligned" in msg
+    bad = _group_args(ns)
+    bad.y[1] = None
+    rc, msg = _lib.gemv_group_check(bad)
+    assert rc == -1 and "non-NULL" in msg
+    bad = _group_args(ns)
+    bad.y_stride[2] = 100
+    rc, msg = _lib.gemv_group_check(bad)
+    assert rc == -1 and "y_stride" in msg
+    _lib.gemv_group(_group_args(ns, m=0, x=None), 0)  # empty: no-op
 
 
 def test_rmsnorm_and_matmul_validation_cpu():

@@ -81,3 +81,126 @@ def test_matmul(M, K, N, dtype):
     ref = (a.double() @ b.double())
     tol = 1e-3 * K ** 0.5 if dtype == torch.float32 else 2e-2 * K ** 0.5
     torch.testing.assert_close(c.double(), ref, atol=tol, rtol=1e-2)
+
+
+def _assert_one_rounding(c, a, b):
+    """c must be the fp32 product rounded once to c's dtype: within one ulp of
+    the dtype (2^-7 relative for bf16, 2^-10 for fp16) of the fp64 product,
+    plus the fp32 accumulation error of a K-term sum."""
+    ref = a.double() @ b.double()
+    K = a.shape[1]
+    rel = 2.0 ** -7 if c.dtype == torch.bfloat16 else 2.0 ** -10
+    bound = ref.abs() * rel + 4 * K * 2.0 ** -24 * (a.double().abs() @ b.double().abs()) + 1e-30
+    err = (c.double() - ref).abs()
+    assert (err <= bound).all(), f"max excess {(err - bound).max().item():.3e}"
+
+
+SKINNY_KN = [(4096, 4096), (4096, 1024), (14336, 4096), (4096, 14336), (100, 8), (1, 8), (4097, 4104),
+             (20000, 264), (2048, 128256)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("K,N", SKINNY_KN)
+def test_skinny_matmul_all_row_counts(K, N, dtype):
+    """lsfa_gemv for 1..8 rows (capacities 1/2/4/8, and 3, 5-7 through the
+    next one up) against the fp64 product, one rounding from fp32."""
+    from lightserve_amd.kernels.tiled_matmul import skinny_matmul
+    print(f"case gemv K={K} N={N} {dtype}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(K + N)
+    b = (torch.randn(K, N, device="cuda", generator=g) / K ** 0.5).to(dtype)
+    for M in range(1, 9):
+        a = torch.randn(M, K, device="cuda", generator=g).to(dtype)
+        c = skinny_matmul(a, b)
+        torch.cuda.synchronize()
+        _assert_one_rounding(c, a, b)
+
+
+def test_skinny_matmul_strided_and_dispatch():
+    """Row strides on x, w and y; matmul routes M <= 8 to the skinny kernel
+    (bit-identical) and larger M to hipBLASLt; results are deterministic."""
+    from lightserve_amd.kernels.tiled_matmul import skinny_matmul
+    print("case gemv strided / dispatch", flush=True)
+    torch.manual_seed(3)
+    xb = torch.randn(6, 3000, device="cuda", dtype=torch.bfloat16)
+    wb = (torch.randn(2500, 1104, device="cuda") / 50).to(torch.bfloat16)
+    x, w = xb[:, 5:2505], wb[:, 8:1032]        # x misaligned start, w rows 16-byte aligned
+    yb = torch.zeros(6, 1200, device="cuda", dtype=torch.bfloat16)
+    y = skinny_matmul(x, w, out=yb[:, 16:1040])
+    torch.cuda.synchronize()
+    _assert_one_rounding(y, x, w)
+    assert (yb[:, :16] == 0).all() and (yb[:, 1040:] == 0).all()
+    assert torch.equal(matmul(x, w), y) and torch.equal(skinny_matmul(x, w), y)
+    big = torch.randn(9, 2500, device="cuda", dtype=torch.bfloat16)
+    torch.testing.assert_close(matmul(big, w).float(), (big.float() @ w.float()), atol=5e-2, rtol=2e-2)
+    assert skinny_matmul(x[:, :0], w[:0]).abs().sum() == 0  # K = 0: zeros
+
+
+def test_skinny_matmul_in_graph_replays():
+    """Captured in a HIP graph, every replay matches the eager result (the
+    workspace comes from the graph's pool; no memsets are recorded)."""
+    from lightserve_amd.kernels.tiled_matmul import skinny_matmul
+    print("case gemv graph", flush=True)
+    torch.manual_seed(4)
+    x = torch.randn(4, 4096, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(4096, 4096, device="cuda") / 64).to(torch.bfloat16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        skinny_matmul(x, w)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = skinny_matmul(x, w)
+    for i in range(4):
+        x.copy_(torch.randn(4, 4096, device="cuda", dtype=torch.bfloat16))
+        eager = skinny_matmul(x, w)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {i}"
+
+
+def test_skinny_matmul_counters_return_to_zero():
+    """The last workgroup of each column block clears its arrival counter:
+    after calls of several shapes the stream's workspace counters read zero,
+    and repeated calls give bit-identical results."""
+    from lightserve_amd.kernels import tiled_matmul
+    print("case gemv counters", flush=True)
+    torch.manual_seed(5)
+    for M, K, N in [(3, 4096, 4096), (1, 14336, 4096), (8, 4096, 14336), (2, 4096, 128256)]:
+        x = torch.randn(M, K, device="cuda", dtype=torch.bfloat16)
+        w = (torch.randn(K, N, device="cuda") / K ** 0.5).to(torch.bfloat16)
+        first = tiled_matmul.skinny_matmul(x, w)
+        again = tiled_matmul.skinny_matmul(x, w)
+        torch.cuda.synchronize()
+        assert torch.equal(first, again), (M, K, N)
+        ws = tiled_matmul._workspaces[(0, torch.cuda.current_stream().cuda_stream)][-1]
+        blocks = (N + 255) // 256
+        assert (ws[:blocks * 64] == 0).all(), (M, K, N)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_skinny_matmul_group(M):
+    """One grouped launch over matrices of widths that do not divide into
+    256-column blocks (blocks straddle matrices), with strided outputs; the
+    decoder's q/k/v and gate/up groups through matmul_shared_input."""
+    from lightserve_amd.kernels.tiled_matmul import matmul_shared_input, skinny_matmul_group
+    print(f"case gemv group M={M}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(M)
+    K = 3000
+    a = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    bs = [(torch.randn(K, n, device="cuda", generator=g) / K ** 0.5).to(torch.bfloat16) for n in (264, 8, 1000, 128)]
+    big = torch.zeros(M, 2000, device="cuda", dtype=torch.bfloat16)
+    outs = [torch.empty(M, 264, device="cuda", dtype=torch.bfloat16), big[:, 8:16],
+            big[:, 16:1016], torch.empty(M, 128, device="cuda", dtype=torch.bfloat16)]
+    res = skinny_matmul_group(a, bs, outs)
+    torch.cuda.synchronize()
+    for c, b in zip(res, bs):
+        _assert_one_rounding(c, a, b)
+    assert (big[:, :8] == 0).all() and (big[:, 1016:] == 0).all()
+    H, F = 4096, 14336
+    h = torch.randn(M, H, device="cuda", generator=g).to(torch.bfloat16)
+    for shapes in ([(H, H), (H, 1024), (H, 1024)], [(H, F), (H, F)]):
+        ws = [(torch.randn(*s, device="cuda", generator=g) / H ** 0.5).to(torch.bfloat16) for s in shapes]
+        for c, w in zip(matmul_shared_input(h, ws), ws):
+            _assert_one_rounding(c, h, w)
