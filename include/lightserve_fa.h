@@ -328,13 +328,19 @@ typedef struct {
  * matrices that share x (and so K), e.g. a decoder's q/k/v or gate/up
  * projections, as one launch over their concatenated columns. Each w_i / y_i
  * follows the rules of lsfa_gemv_args; the workspace (counters, then partials
- * of all columns) follows them for n = n[0] + ... + n[count-1]. */
+ * of all columns) follows them for n = n[0] + ... + n[count-1].
+ * x_gate (optional, NULL for none; [M, K] with row stride x_gate_stride):
+ * the products read silu(x_gate) * x instead of x, each rounded to the dtype
+ * as torch rounds F.silu(gate) * up (the SwiGLU input of a down projection,
+ * model/minimal_llama.py's mlp). */
 #define LSFA_GEMV_MAX_GROUP 4
 typedef struct {
   const void* x;
   void* workspace;
   uint64_t workspace_bytes;
   int64_t x_stride;
+  const void* x_gate;
+  int64_t x_gate_stride;
   const void* w[LSFA_GEMV_MAX_GROUP];
   void* y[LSFA_GEMV_MAX_GROUP];
   int64_t w_stride[LSFA_GEMV_MAX_GROUP];
@@ -345,6 +351,24 @@ typedef struct {
   int32_t k;
   int32_t count;
 } lsfa_gemv_group_args;
+
+/* Greedy next token of a decode step: tokens[r] = argmax over logits[r, :]
+ * (comparison as torch's argmax: NaN beats every number, ties go to the
+ * lower index) and, when seq_lens is non-NULL, seq_lens[r] += 1. Replaces the
+ * reference's torch argmax and length update after each step
+ * (model/cuda_graph_decode.py:114, :145).
+ *   logits [rows, cols] fp32/fp16/bf16, row stride in elements, columns
+ *   contiguous; tokens int64 [rows]; seq_lens int32 [rows] or NULL */
+typedef struct {
+  const void* logits;
+  int64_t* tokens;
+  int32_t* seq_lens;
+  int64_t logits_stride;
+  int32_t dtype;
+  int32_t rows;
+  int32_t cols;
+  int32_t reserved;
+} lsfa_greedy_args;
 
 /* ABI version of the loaded library (LSFA_ABI_VERSION). */
 int lsfa_abi_version(void);
@@ -415,6 +439,12 @@ int lsfa_gemv(const lsfa_gemv_args* args, void* stream);
 int lsfa_gemv_group_check(const lsfa_gemv_group_args* args);
 int lsfa_gemv_group_workspace_size(const lsfa_gemv_group_args* args, uint64_t* bytes);
 int lsfa_gemv_group(const lsfa_gemv_group_args* args, void* stream);
+
+/* Host-only validation of greedy-token arguments; never touches the GPU. */
+int lsfa_greedy_check(const lsfa_greedy_args* args);
+
+/* Greedy next token (see lsfa_greedy_args): one launch, one workgroup per row. */
+int lsfa_greedy(const lsfa_greedy_args* args, void* stream);
 
 /* Host-only validation of RMSNorm arguments; never touches the GPU. */
 int lsfa_rmsnorm_check(const lsfa_rmsnorm_args* args);

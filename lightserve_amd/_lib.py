@@ -26,7 +26,8 @@ EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "ls
                     "lsfa_rope_check", "lsfa_rope", "lsfa_rmsnorm_check", "lsfa_rmsnorm",
                     "lsfa_prefill_paged_check", "lsfa_prefill_paged",
                     "lsfa_gemv_check", "lsfa_gemv_workspace_size", "lsfa_gemv",
-                    "lsfa_gemv_group_check", "lsfa_gemv_group_workspace_size", "lsfa_gemv_group")
+                    "lsfa_gemv_group_check", "lsfa_gemv_group_workspace_size", "lsfa_gemv_group",
+                    "lsfa_greedy_check", "lsfa_greedy")
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -111,17 +112,27 @@ class GemvArgs(ctypes.Structure):
 
 
 GEMV_MAX_GROUP = 4
+GEMV_COUNTER_BYTES = 262144  # LSFA_GEMV_COUNTER_BYTES
 
 
 class GemvGroupArgs(ctypes.Structure):
     """Mirror of lsfa_gemv_group_args."""
     _fields_ = [
         ("x", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64),
-        ("x_stride", ctypes.c_int64),
+        ("x_stride", ctypes.c_int64), ("x_gate", ctypes.c_void_p), ("x_gate_stride", ctypes.c_int64),
         ("w", ctypes.c_void_p * GEMV_MAX_GROUP), ("y", ctypes.c_void_p * GEMV_MAX_GROUP),
         ("w_stride", ctypes.c_int64 * GEMV_MAX_GROUP), ("y_stride", ctypes.c_int64 * GEMV_MAX_GROUP),
         ("n", ctypes.c_int32 * GEMV_MAX_GROUP),
         ("dtype", ctypes.c_int32), ("m", ctypes.c_int32), ("k", ctypes.c_int32), ("count", ctypes.c_int32),
+    ]
+
+
+class GreedyArgs(ctypes.Structure):
+    """Mirror of lsfa_greedy_args."""
+    _fields_ = [
+        ("logits", ctypes.c_void_p), ("tokens", ctypes.c_void_p), ("seq_lens", ctypes.c_void_p),
+        ("logits_stride", ctypes.c_int64), ("dtype", ctypes.c_int32), ("rows", ctypes.c_int32),
+        ("cols", ctypes.c_int32), ("reserved", ctypes.c_int32),
     ]
 
 
@@ -176,14 +187,15 @@ def load():
         for name, struct in (("lsfa_fwd_check", FwdArgs), ("lsfa_bwd_check", BwdArgs),
                              ("lsfa_decode_check", DecodeArgs), ("lsfa_rope_check", RopeArgs),
                              ("lsfa_rmsnorm_check", RmsNormArgs), ("lsfa_prefill_paged_check", PrefillPagedArgs),
-                             ("lsfa_gemv_check", GemvArgs), ("lsfa_gemv_group_check", GemvGroupArgs)):
+                             ("lsfa_gemv_check", GemvArgs), ("lsfa_gemv_group_check", GemvGroupArgs),
+                             ("lsfa_greedy_check", GreedyArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct)]
         for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_decode", DecodeArgs),
                              ("lsfa_rope", RopeArgs), ("lsfa_rmsnorm", RmsNormArgs),
                              ("lsfa_prefill_paged", PrefillPagedArgs), ("lsfa_gemv", GemvArgs),
-                             ("lsfa_gemv_group", GemvGroupArgs)):
+                             ("lsfa_gemv_group", GemvGroupArgs), ("lsfa_greedy", GreedyArgs)):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
@@ -287,6 +299,16 @@ def gemv_group_workspace_size(args):
 
 def gemv_group(args, stream):
     _raise_on(load().lsfa_gemv_group(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_gemv_group")
+
+
+def greedy_check(args):
+    """Host-only validation (no GPU access); returns (status, message)."""
+    rc = load().lsfa_greedy_check(ctypes.byref(args))
+    return rc, load().lsfa_last_error().decode(errors="replace")
+
+
+def greedy(args, stream):
+    _raise_on(load().lsfa_greedy(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_greedy")
 
 
 def rope_check(args):

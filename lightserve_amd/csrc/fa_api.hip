@@ -21,6 +21,8 @@ hipError_t rope_inplace(const RopeParams& p, int dtype, hipStream_t s);
 hipError_t add_rmsnorm(const NormParams& p, int dtype, bool vec, hipStream_t s);
 hipError_t gemv(const GemvParams& p, bool is_bf16, hipStream_t s);
 int gemv_capacity(int m);
+hipError_t greedy(const void* logits, int64_t stride, int dtype, int rows, int cols, int64_t* tokens,
+                  int32_t* seq_lens, hipStream_t s);
 }  // namespace lsfa
 
 namespace {
@@ -511,6 +513,7 @@ int lsfa_gemv_group_check(const lsfa_gemv_group_args* a) {
   if (a->m == 0 || N == 0) return ok();
   if (!a->x) return fail(LSFA_ERR_INVALID, "x, w and y must be non-NULL");
   if (a->x_stride < a->k) return fail(LSFA_ERR_INVALID, "x_stride must be >= k");
+  if (a->x_gate && a->x_gate_stride < a->k) return fail(LSFA_ERR_INVALID, "x_gate_stride must be >= k");
   for (int i = 0; i < a->count; ++i) {
     if (a->n[i] == 0) continue;
     if (!a->w[i] || !a->y[i]) return fail(LSFA_ERR_INVALID, "x, w and y must be non-NULL");
@@ -546,6 +549,8 @@ int lsfa_gemv_group(const lsfa_gemv_group_args* a, void* stream) {
   lsfa::GemvParams p;
   memset(&p, 0, sizeof(p));
   p.x = a->x;
+  p.xg = a->x_gate;
+  p.sxg = a->x_gate_stride;
   int off = 0;
   for (int i = 0; i < 4; ++i) {
     p.col_off[i] = off;
@@ -585,6 +590,28 @@ int lsfa_gemv(const lsfa_gemv_args* a, void* stream) {
   if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
   const lsfa_gemv_group_args gr = gemv_as_group(a);
   return lsfa_gemv_group(&gr, stream);
+}
+
+int lsfa_greedy_check(const lsfa_greedy_args* a) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  if (a->dtype != LSFA_DTYPE_FP32 && a->dtype != LSFA_DTYPE_FP16 && a->dtype != LSFA_DTYPE_BF16)
+    return fail(LSFA_ERR_INVALID, "unknown dtype %d", a->dtype);
+  if (a->rows < 0 || a->cols < 0) return fail(LSFA_ERR_INVALID, "negative size (rows=%d cols=%d)", a->rows, a->cols);
+  if (a->rows > 65535) return fail(LSFA_ERR_UNSUPPORTED, "at most 65535 rows per call (rows=%d)", a->rows);
+  if (a->rows == 0) return ok();
+  if (a->cols == 0) return fail(LSFA_ERR_INVALID, "argmax of an empty row");
+  if (!a->logits || !a->tokens) return fail(LSFA_ERR_INVALID, "logits and tokens must be non-NULL");
+  if (a->logits_stride < a->cols) return fail(LSFA_ERR_INVALID, "logits_stride must be >= cols");
+  return ok();
+}
+
+int lsfa_greedy(const lsfa_greedy_args* a, void* stream) {
+  int rc = lsfa_greedy_check(a);
+  if (rc) return rc;
+  hipError_t e = lsfa::greedy(a->logits, a->logits_stride, a->dtype, a->rows, a->cols, a->tokens, a->seq_lens,
+                              reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "greedy launch failed: %s", hipGetErrorString(e));
+  return ok();
 }
 
 int lsfa_rope_check(const lsfa_rope_args* a) {

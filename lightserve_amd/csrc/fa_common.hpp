@@ -194,6 +194,8 @@ struct GemvParams {
   // one after another (matrix g holds columns col_off[g] .. col_off[g+1]-1 of
   // a virtual y of N = col_off[groups] columns).
   const void* x;
+  const void* xg;  // optional gate: the product reads bf16/fp16(silu(xg) * x), as torch rounds it
+  int64_t sxg;
   const void* w[4];
   void* y[4];
   int64_t sw[4], sy[4];

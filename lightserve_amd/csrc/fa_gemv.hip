@@ -71,10 +71,48 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
   const int split = blockIdx.y;
   const int k_begin = split * p.kc;
   const int k_len = max(0, min(p.K, k_begin + p.kc) - k_begin);
+  // This thread's rows of W: kg, kg + 8, ... of the K-range, in batches of
+  // eight (one 16-byte load each, all issued before the first use). The
+  // first batch is in flight before x is staged, so the two latencies
+  // overlap.
+  const bool has_cols = n0 < p.N;
+  const int rows_t = (has_cols && kg < k_len) ? (k_len - kg + kGemvKG - 1) / kGemvKG : 0;
+  const int full = rows_t >> 3, rem = rows_t & 7;
+  const T* wp = nullptr;
+  int64_t step = 0;
+  if (has_cols) {
+    const int g = gemv_group(p, n0);
+    const int64_t sw = gemv_pick(g, p.sw[0], p.sw[1], p.sw[2], p.sw[3]);
+    wp = (const T*)gemv_pick(g, p.w[0], p.w[1], p.w[2], p.w[3]) + (int64_t)(k_begin + kg) * sw +
+         (n0 - gemv_pick(g, p.col_off[0], p.col_off[1], p.col_off[2], p.col_off[3]));
+    step = (int64_t)kGemvKG * sw;
+  }
+  u32x4 cur[8];
+  if (full > 0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cur[u] = __builtin_nontemporal_load((const u32x4*)(wp + u * step));
+    wp += 8 * step;
+  }
+
   float* xs = gemv_smem;
-  for (int idx = tid; idx < M * k_len; idx += 256) {
-    const int m = idx / k_len, k = idx - m * k_len;
-    xs[m * p.kc + k] = m < p.M ? (float)((const T*)p.x)[(int64_t)m * p.sx + k_begin + k] : 0.f;
+  if (p.xg == nullptr) {
+    for (int idx = tid; idx < M * k_len; idx += 256) {
+      const int m = idx / k_len, k = idx - m * k_len;
+      xs[m * p.kc + k] = m < p.M ? (float)((const T*)p.x)[(int64_t)m * p.sx + k_begin + k] : 0.f;
+    }
+  } else {
+    // SwiGLU input: silu(gate) rounded to T, times x rounded to T (the two
+    // roundings of F.silu(gate) * up on bf16/fp16 tensors).
+    for (int idx = tid; idx < M * k_len; idx += 256) {
+      const int m = idx / k_len, k = idx - m * k_len;
+      float v = 0.f;
+      if (m < p.M) {
+        const float g = (float)((const T*)p.xg)[(int64_t)m * p.sxg + k_begin + k];
+        const float act = (float)(T)(g / (1.0f + expf(-g)));
+        v = (float)(T)(act * (float)((const T*)p.x)[(int64_t)m * p.sx + k_begin + k]);
+      }
+      xs[m * p.kc + k] = v;
+    }
   }
   __syncthreads();
 
@@ -94,36 +132,32 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
     }
   };
 
-  if (n0 < p.N) {
-    const int g = gemv_group(p, n0);
-    const int64_t sw = gemv_pick(g, p.sw[0], p.sw[1], p.sw[2], p.sw[3]);
-    const T* wp = (const T*)gemv_pick(g, p.w[0], p.w[1], p.w[2], p.w[3]) + (int64_t)(k_begin + kg) * sw +
-                  (n0 - gemv_pick(g, p.col_off[0], p.col_off[1], p.col_off[2], p.col_off[3]));
-    const int64_t step = (int64_t)kGemvKG * sw;
-    int k = kg;
-    for (; k + 7 * kGemvKG < k_len; k += 8 * kGemvKG) {  // eight rows in flight
-      u32x4 raw[8];
+  int k = kg;
+  for (int b = 0; b < full; ++b) {
+    if (b > 0) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) raw[u] = __builtin_nontemporal_load((const u32x4*)(wp + u * step));
-      __builtin_amdgcn_sched_barrier(0);  // all eight loads issue before the first use
+      for (int u = 0; u < 8; ++u) cur[u] = __builtin_nontemporal_load((const u32x4*)(wp + u * step));
       wp += 8 * step;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) fma_row(raw[u], k + u * kGemvKG);
+      __builtin_amdgcn_sched_barrier(0);  // all eight loads issue before the first use
     }
-    if (k + 3 * kGemvKG < k_len) {
-      u32x4 raw[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) raw[u] = __builtin_nontemporal_load((const u32x4*)(wp + u * step));
-      __builtin_amdgcn_sched_barrier(0);
-      wp += 4 * step;
+    for (int u = 0; u < 8; ++u) fma_row(cur[u], k + u * kGemvKG);
+    k += 8 * kGemvKG;
+  }
+  if (rem >= 4) {
+    u32x4 r4[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) fma_row(raw[u], k + u * kGemvKG);
-      k += 4 * kGemvKG;
-    }
-    for (; k < k_len; k += kGemvKG) {
-      fma_row(__builtin_nontemporal_load((const u32x4*)wp), k);
-      wp += step;
-    }
+    for (int u = 0; u < 4; ++u) r4[u] = __builtin_nontemporal_load((const u32x4*)(wp + u * step));
+    __builtin_amdgcn_sched_barrier(0);
+    wp += 4 * step;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fma_row(r4[u], k + u * kGemvKG);
+    k += 4 * kGemvKG;
+  }
+  for (int u = 0; u < (rem & 3); ++u) {
+    fma_row(__builtin_nontemporal_load((const u32x4*)wp), k);
+    wp += step;
+    k += kGemvKG;
   }
 
   // Sum the K-groups: red[kg][m][column] over the x chunk.

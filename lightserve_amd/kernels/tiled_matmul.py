@@ -8,28 +8,36 @@ model code and the reference's tests call it unchanged. fp32 operands use
 IEEE fp32 (torch's default, allow_tf32 off), as the reference's
 input_precision="ieee" does.
 
-Decode-time calls carry 1..8 rows (one per sequence in the batch). There a
-GEMM is a single pass over B's bytes, so bf16/fp16 products with M <= 8 go to
-the library's skinny kernel (lsfa_gemv: one launch, a K-split pass over B at
-HBM rate whose last workgroup per column block sums the fp32 partials and
-rounds once), which hipBLASLt's general tiles reach at a fraction of the
-bandwidth.
+Decode-time calls carry one row per sequence in the batch. There a GEMM is a
+single pass over B's bytes, so bf16/fp16 products with M <= 2 go to the
+library's skinny kernel (lsfa_gemv: one launch, a K-split pass over B at HBM
+rate whose last workgroup per column block sums the fp32 partials and rounds
+once), which hipBLASLt's general tiles reach at a fraction of the bandwidth.
+The kernel takes up to 8 rows (skinny_matmul), but its fp32 FMAs grow with
+the row count and, measured on MI355X over the LLaMA-3-8B decode projections,
+hipBLASLt overtakes it on some shapes from 3 rows on, so the automatic
+routing stops at 2.
 
 Projections that share their input (a decoder's q/k/v, gate/up) go through
 matmul_shared_input, which runs them as one lsfa_gemv_group launch over their
 concatenated columns when they qualify for the skinny kernel.
 
-lsfa_gemv's workspace carries arrival counters that must start at zero and
-that every call leaves at zero, so this module keeps one zero-initialised
-workspace per (device, stream) and reuses it for every call on that stream
-(stream order keeps the calls apart). A workspace that grows is replaced, not
-freed: a captured HIP graph that recorded the old one keeps using it.
+lsfa_gemv's workspace carries arrival counters (its first
+LSFA_GEMV_COUNTER_BYTES) that must start at zero and that every call leaves
+at zero, so this module keeps one workspace per (device, stream), zeroes its
+counter bytes once when it is created, and reuses it for every call on that
+stream (stream order keeps the calls apart). Workspaces start at 16 MB, so
+they rarely grow; one that grows is replaced, not freed: a captured HIP graph
+that recorded the old one keeps using it. (A workspace first created inside
+a graph capture records its counter fill into the graph, which then clears
+the 256 KB on every replay.)
 """
 import torch
 
 from .. import _lib
 
-SKINNY_MAX_ROWS = 8
+SKINNY_MAX_ROWS = 8  # what lsfa_gemv takes
+AUTO_MAX_ROWS = 2    # what matmul, matmul_shared_input and swiglu_matmul route to it
 
 _workspaces = {}  # (device index, stream handle) -> every workspace created for it, the last in use
 
@@ -37,12 +45,14 @@ _workspaces = {}  # (device index, stream handle) -> every workspace created for
 def _workspace(device, stream, nbytes):
     bufs = _workspaces.setdefault((device.index, stream), [])
     if not bufs or bufs[-1].numel() < nbytes:
-        bufs.append(torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device))
+        buf = torch.empty(max(nbytes, 16 << 20), dtype=torch.uint8, device=device)
+        buf[:_lib.GEMV_COUNTER_BYTES].zero_()
+        bufs.append(buf)
     return bufs[-1]
 
 
-def _skinny_ok(a: torch.Tensor, b: torch.Tensor) -> bool:
-    return (a.shape[0] <= SKINNY_MAX_ROWS and a.dtype in (torch.bfloat16, torch.float16)
+def _skinny_ok(a: torch.Tensor, b: torch.Tensor, max_rows: int = SKINNY_MAX_ROWS) -> bool:
+    return (a.shape[0] <= max_rows and a.dtype in (torch.bfloat16, torch.float16)
             and a.stride(1) == 1 and b.stride(1) == 1 and b.shape[1] % 8 == 0
             and b.stride(0) % 8 == 0 and b.stride(0) >= b.shape[1] and b.data_ptr() % 16 == 0)
 
@@ -72,10 +82,14 @@ def skinny_matmul(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor = None) ->
     return out
 
 
-def skinny_matmul_group(a: torch.Tensor, bs, outs=None):
+def skinny_matmul_group(a: torch.Tensor, bs, outs=None, gate: torch.Tensor = None):
     """[a @ b for b in bs] for up to four b sharing a (each as for
-    skinny_matmul) in one lsfa_gemv_group launch."""
+    skinny_matmul) in one lsfa_gemv_group launch. With gate (a's shape and
+    dtype), the products read F.silu(gate) * a instead of a, rounded as torch
+    rounds it."""
     assert 1 <= len(bs) <= _lib.GEMV_MAX_GROUP, f"1..{_lib.GEMV_MAX_GROUP} matrices per group"
+    assert gate is None or (gate.shape == a.shape and gate.dtype == a.dtype and gate.stride(1) == 1), (
+        "gate must match a's shape and dtype, with unit column stride")
     assert all(_skinny_ok(a, b) and b.shape[0] == a.shape[1] and b.dtype == a.dtype for b in bs), (
         "every matrix must qualify for skinny_matmul with the shared input")
     M, K = a.shape
@@ -87,6 +101,8 @@ def skinny_matmul_group(a: torch.Tensor, bs, outs=None):
         return [o.zero_() for o in outs]
     args = _lib.GemvGroupArgs(x=a.data_ptr(), x_stride=a.stride(0), dtype=_lib.TORCH_TO_LSFA[a.dtype], m=M, k=K,
                               count=len(bs))
+    if gate is not None:
+        args.x_gate, args.x_gate_stride = gate.data_ptr(), gate.stride(0)
     for i, (b, o) in enumerate(zip(bs, outs)):
         args.w[i], args.y[i] = b.data_ptr(), o.data_ptr()
         args.w_stride[i], args.y_stride[i], args.n[i] = b.stride(0), o.stride(0), b.shape[1]
@@ -104,10 +120,19 @@ def matmul_shared_input(a: torch.Tensor, bs):
     """[matmul(a, b) for b in bs]: one grouped skinny launch when every
     product qualifies for the skinny kernel, else one matmul each."""
     if len(bs) <= _lib.GEMV_MAX_GROUP and a.ndim == 2 and a.is_cuda and all(
-            b.ndim == 2 and b.is_cuda and b.dtype == a.dtype and b.shape[0] == a.shape[1] and _skinny_ok(a, b)
-            for b in bs):
+            b.ndim == 2 and b.is_cuda and b.dtype == a.dtype and b.shape[0] == a.shape[1]
+            and _skinny_ok(a, b, AUTO_MAX_ROWS) for b in bs):
         return skinny_matmul_group(a, bs)
     return [matmul(a, b) for b in bs]
+
+
+def swiglu_matmul(gate: torch.Tensor, up: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """matmul(F.silu(gate) * up, b), the activation folded into the skinny
+    kernel's load of its input when the product qualifies for it."""
+    if (gate.ndim == 2 and gate.shape == up.shape and gate.dtype == up.dtype == b.dtype and gate.is_cuda
+            and b.ndim == 2 and b.shape[0] == up.shape[1] and gate.stride(1) == 1 and _skinny_ok(up, b, AUTO_MAX_ROWS)):
+        return skinny_matmul_group(up, [b], gate=gate)[0]
+    return matmul(torch.nn.functional.silu(gate) * up, b)
 
 
 def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -116,6 +141,6 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     assert a.shape[1] == b.shape[0], f"inner dims must match: a is {tuple(a.shape)}, b is {tuple(b.shape)}"
     assert a.is_cuda and b.is_cuda, "the gfx950 path needs GPU tensors"
     assert a.dtype == b.dtype, f"dtype mismatch: a={a.dtype} b={b.dtype}"
-    if _skinny_ok(a, b):
+    if _skinny_ok(a, b, AUTO_MAX_ROWS):
         return skinny_matmul(a, b)
     return torch.matmul(a, b)

@@ -32,7 +32,8 @@ import torch.nn.functional as F
 from ..kernels.paged_attention import paged_attention_decode, paged_prefill
 from ..kernels.rope import apply_rope_
 from ..kernels.fused_rmsnorm_residual import fused_add_rmsnorm
-from ..kernels.tiled_matmul import matmul, matmul_shared_input
+from ..kernels.greedy import greedy_next_token
+from ..kernels.tiled_matmul import matmul, matmul_shared_input, swiglu_matmul
 from .minimal_llama import add_norm, init_weights, llama3_8b_shape, llama_forward, precompute_rope
 
 SEED_TOKEN_ID = 1
@@ -154,7 +155,7 @@ class KVCacheDecoder:
             h2, residual = fused_add_rmsnorm(matmul(o.view(B, nh * hd), layer.o_proj), residual,
                                              layer.post_attention_layernorm_weight, cfg.rms_eps)
             gate, up = matmul_shared_input(h2, (layer.gate_proj, layer.up_proj))
-            pending = matmul(F.silu(gate) * up, layer.down_proj)
+            pending = swiglu_matmul(gate, up, layer.down_proj)
         final, _ = add_norm(pending, residual, self.w.norm_weight, cfg.rms_eps)
         return matmul(final, self.w.lm_head)
 
@@ -199,13 +200,12 @@ class KVCacheDecoder:
                                 residual[last].contiguous(), self.w.norm_weight, cfg.rms_eps)
             logits = matmul(final, self.w.lm_head)
             self.seq_lens.add_(c)
-        self.tokens.copy_(logits.argmax(dim=-1))
+        greedy_next_token(logits, out=self.tokens)
         return logits
 
     def advance(self, logits):
-        """Greedy next token; one more cached token per sequence."""
-        self.tokens.copy_(logits.argmax(dim=-1))
-        self.seq_lens.add_(1)
+        """Greedy next token; one more cached token per sequence (one launch)."""
+        greedy_next_token(logits, out=self.tokens, seq_lens=self.seq_lens)
         return self.tokens
 
 

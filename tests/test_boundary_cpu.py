@@ -426,6 +426,13 @@ def _group_args(ns, **kw):
     return a
 
 
+def test_gemv_constants_match_header():
+    import re
+    text = open(HEADER).read()
+    assert int(re.search(r"#define LSFA_GEMV_COUNTER_BYTES (\d+)", text).group(1)) == _lib.GEMV_COUNTER_BYTES
+    assert int(re.search(r"#define LSFA_GEMV_MAX_GROUP (\d+)", text).group(1)) == _lib.GEMV_MAX_GROUP
+
+
 def test_abi_gemv_group_validation(built_library):
     """The grouped skinny GEMM: validation per matrix, workspace sized for
     the concatenated columns (the same as one matrix of that width)."""
@@ -433,6 +440,9 @@ def test_abi_gemv_group_validation(built_library):
     assert _lib.gemv_group_check(_group_args(ns))[0] == 0
     assert _lib.gemv_group_workspace_size(_group_args(ns)) == _lib.gemv_workspace_size(
         _gemv_args(m=2, k=4096, n=sum(ns)))
+    rc, msg = _lib.gemv_group_check(_group_args(ns, x_gate=8192, x_gate_stride=100))
+    assert rc == -1 and "x_gate_stride" in msg
+    assert _lib.gemv_group_check(_group_args(ns, x_gate=8192, x_gate_stride=4096))[0] == 0
     rc, msg = _lib.gemv_group_check(_group_args(ns, count=5))
     assert rc == -1 and "count" in msg
     rc, msg = _lib.gemv_group_check(_group_args(ns, count=0))
@@ -453,6 +463,18 @@ def test_abi_gemv_group_validation(built_library):
     rc, msg = _lib.gemv_group_check(bad)
     assert rc == -1 and "y_stride" in msg
     _lib.gemv_group(_group_args(ns, m=0, x=None), 0)  # empty: no-op
+
+
+def test_abi_greedy_validation(built_library):
+    base = dict(logits=4096, tokens=8192, seq_lens=None, logits_stride=128256, dtype=_lib.DTYPE_BF16, rows=4,
+                cols=128256)
+    assert _lib.greedy_check(_lib.GreedyArgs(**base))[0] == 0
+    for kw, code, word in [(dict(cols=0), -1, "empty"), (dict(logits_stride=100), -1, "logits_stride"),
+                           (dict(dtype=9), -1, "dtype"), (dict(tokens=None), -1, "non-NULL"),
+                           (dict(rows=70000), -2, "rows")]:
+        rc, msg = _lib.greedy_check(_lib.GreedyArgs(**{**base, **kw}))
+        assert rc == code and word in msg, (kw, rc, msg)
+    _lib.greedy(_lib.GreedyArgs(**{**base, "rows": 0, "logits": None}), 0)  # empty: no-op
 
 
 def test_rmsnorm_and_matmul_validation_cpu():

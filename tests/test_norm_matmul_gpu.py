@@ -116,7 +116,7 @@ def test_skinny_matmul_all_row_counts(K, N, dtype):
 
 
 def test_skinny_matmul_strided_and_dispatch():
-    """Row strides on x, w and y; matmul routes M <= 8 to the skinny kernel
+    """Row strides on x, w and y; matmul routes M <= 2 to the skinny kernel
     (bit-identical) and larger M to hipBLASLt; results are deterministic."""
     from lightserve_amd.kernels.tiled_matmul import skinny_matmul
     print("case gemv strided / dispatch", flush=True)
@@ -129,8 +129,9 @@ def test_skinny_matmul_strided_and_dispatch():
     torch.cuda.synchronize()
     _assert_one_rounding(y, x, w)
     assert (yb[:, :16] == 0).all() and (yb[:, 1040:] == 0).all()
-    assert torch.equal(matmul(x, w), y) and torch.equal(skinny_matmul(x, w), y)
-    big = torch.randn(9, 2500, device="cuda", dtype=torch.bfloat16)
+    assert torch.equal(skinny_matmul(x, w), y)
+    assert torch.equal(matmul(x[:2], w), skinny_matmul(x[:2], w))
+    big = torch.randn(3, 2500, device="cuda", dtype=torch.bfloat16)
     torch.testing.assert_close(matmul(big, w).float(), (big.float() @ w.float()), atol=5e-2, rtol=2e-2)
     assert skinny_matmul(x[:, :0], w[:0]).abs().sum() == 0  # K = 0: zeros
 
@@ -204,3 +205,30 @@ def test_skinny_matmul_group(M):
         ws = [(torch.randn(*s, device="cuda", generator=g) / H ** 0.5).to(torch.bfloat16) for s in shapes]
         for c, w in zip(matmul_shared_input(h, ws), ws):
             _assert_one_rounding(c, h, w)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_swiglu_matmul(M):
+    """The SwiGLU input folded into the skinny kernel's load equals
+    matmul(F.silu(gate) * up, w) computed by torch ops then the same kernel
+    (same rounding of the activation and the product), bit for bit;
+    swiglu_matmul routes M <= 2 to it and larger M to torch ops + hipBLASLt."""
+    import torch.nn.functional as F
+    from lightserve_amd.kernels.tiled_matmul import skinny_matmul, skinny_matmul_group, swiglu_matmul
+    print(f"case gemv swiglu M={M}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(10 + M)
+    F_, H = 14336, 4096
+    gate = (torch.randn(M, F_, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    up = torch.randn(M, F_, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(F_, H, device="cuda", generator=g) / F_ ** 0.5).to(torch.bfloat16)
+    fused = skinny_matmul_group(up, [w], gate=gate)[0]
+    x = F.silu(gate) * up
+    ref = skinny_matmul(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, ref)
+    _assert_one_rounding(fused, x, w)
+    routed = swiglu_matmul(gate, up, w)
+    if M <= 2:
+        assert torch.equal(routed, fused)
+    else:
+        torch.testing.assert_close(routed.float(), (x.float() @ w.float()), atol=2e-2, rtol=2e-2)
