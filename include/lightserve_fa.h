@@ -198,7 +198,15 @@ typedef struct {
  *              sequence
  * head_dim must be even with head_dim/2 a multiple of 8 (bf16/fp16) or 4
  * (fp32) elements; stride[3] == 1, other strides multiples of 8 (bf16/fp16)
- * or 4 (fp32) elements, 16-byte aligned pointers. */
+ * or 4 (fp32) elements, 16-byte aligned pointers.
+ * Optional K/V cache append (k_cache non-NULL; the reference model has no
+ * cache, its engine's block layout is engine/block_manager.py:56-60): the
+ * rotated k row and v's row of token t are also stored at slot slots[t] of
+ * k_cache / v_cache ([num_blocks, block_size, heads_kv, head_dim] caches
+ * addressed as slots; cache_stride = elements between slots and between
+ * heads, head-dim stride 1). t = b * seqlen + n, or the packed index with
+ * cu_seqlens. Slots outside [0, num_slots) are skipped (a negative slot marks
+ * a padding token). v has k's shape, v_stride its strides. */
 typedef struct {
   void* q;
   void* k;
@@ -217,6 +225,13 @@ typedef struct {
   int32_t head_dim;
   int32_t max_pos;
   int32_t reserved;
+  const void* v;
+  void* k_cache;
+  void* v_cache;
+  const int64_t* slots;
+  int64_t v_stride[4];
+  int64_t cache_stride[2];
+  int64_t num_slots;
 } lsfa_rope_args;
 
 /* Fused residual add + RMSNorm over the rows of [rows, cols] matrices

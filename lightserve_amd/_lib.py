@@ -149,6 +149,9 @@ class RopeArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("seqlen", ctypes.c_int32),
         ("heads_q", ctypes.c_int32), ("heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("max_pos", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("v", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("slots", ctypes.c_void_p), ("v_stride", _i64x4), ("cache_stride", ctypes.c_int64 * 2),
+        ("num_slots", ctypes.c_int64),
     ]
 
 

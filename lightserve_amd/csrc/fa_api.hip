@@ -647,6 +647,21 @@ int lsfa_rope_check(const lsfa_rope_args* a) {
                     (long long)st[i], vec);
     if (!aligned16(ptr)) return fail(LSFA_ERR_UNSUPPORTED, "%s: base pointer is not 16-byte aligned", name);
   }
+  if (a->k_cache != nullptr) {
+    if (a->heads_kv == 0 || !a->v || !a->v_cache || !a->slots)
+      return fail(LSFA_ERR_INVALID, "a K/V cache append needs heads_kv > 0 and non-NULL v, v_cache and slots");
+    if (a->num_slots < 0) return fail(LSFA_ERR_INVALID, "num_slots must be >= 0");
+    if (a->v_stride[3] != 1 || !aligned16(a->v))
+      return fail(LSFA_ERR_UNSUPPORTED, "v: head-dim stride must be 1 and the pointer 16-byte aligned");
+    for (int i = varlen ? 1 : 0; i < 3; ++i)
+      if (a->v_stride[i] % vec != 0)
+        return fail(LSFA_ERR_UNSUPPORTED, "v: stride[%d] is not a multiple of %d elements", i, vec);
+    if (a->cache_stride[0] < (int64_t)a->heads_kv * a->head_dim || a->cache_stride[1] < a->head_dim ||
+        a->cache_stride[0] % vec != 0 || a->cache_stride[1] % vec != 0 || !aligned16(a->k_cache) ||
+        !aligned16(a->v_cache))
+      return fail(LSFA_ERR_UNSUPPORTED, "caches: slot/head strides must cover a row and be multiples of %d "
+                  "elements, pointers 16-byte aligned", vec);
+  }
   return ok();
 }
 
@@ -665,6 +680,11 @@ int lsfa_rope(const lsfa_rope_args* a, void* stream) {
   p.table_stride = a->table_stride;
   p.B = a->batch; p.N = a->seqlen; p.Hq = a->heads_q; p.Hkv = a->heads_kv; p.D = a->head_dim;
   p.max_pos = a->max_pos;
+  if (a->k_cache != nullptr) {
+    p.v = a->v; p.k_cache = a->k_cache; p.v_cache = a->v_cache; p.slots = a->slots;
+    for (int i = 0; i < 4; ++i) p.sv[i] = a->v_stride[i];
+    p.cs_slot = a->cache_stride[0]; p.cs_head = a->cache_stride[1]; p.num_slots = a->num_slots;
+  }
   hipError_t e = lsfa::rope_inplace(p, a->dtype, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "rope launch failed: %s", hipGetErrorString(e));
   return ok();

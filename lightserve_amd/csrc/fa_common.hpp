@@ -253,6 +253,14 @@ struct RopeParams {
   int64_t sq[4], sk[4];
   int64_t table_stride;
   int B, N, Hq, Hkv, D, max_pos;
+  // Optional K/V cache append: rotated k and v rows of token t go to slot
+  // slots[t] (skipped outside [0, num_slots)).
+  const void* v;
+  void* k_cache;
+  void* v_cache;
+  const int64_t* slots;
+  int64_t sv[4];
+  int64_t cs_slot, cs_head, num_slots;
 };
 
 // Fused residual add + RMSNorm over rows of a [rows, cols] matrix (column

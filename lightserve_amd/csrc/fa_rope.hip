@@ -16,6 +16,10 @@
 // k's, so a token's q and k rows are rotated by neighbouring threads.
 // Positions: token n of sequence b sits at pos0[b] + n (pos0 = 0 when no
 // start positions are given), clamped to the table's rows.
+// With a K/V cache, each rotated k group is also stored at the token's cache
+// slot, and a third run of threads (after q's and k's heads) copies v's
+// groups (both halves) into the v cache: the append of a decode step or a
+// prefill chunk needs no launch of its own.
 #include "fa_common.hpp"
 
 namespace lsfa {
@@ -45,7 +49,8 @@ __global__ __launch_bounds__(256) void fa_rope_kernel(const RopeParams p) {
   const int b = blockIdx.y;
   const int half = p.D / 2;
   const int groups = half / VEC;
-  const int heads = p.Hq + p.Hkv;
+  const bool cache = p.k_cache != nullptr;
+  const int heads = p.Hq + p.Hkv + (cache ? p.Hkv : 0);
   const int64_t per_tok = (int64_t)heads * groups;
   int n_tok = p.N;
   int64_t tok0 = 0;
@@ -60,6 +65,22 @@ __global__ __launch_bounds__(256) void fa_rope_kernel(const RopeParams p) {
   const int hd = rem / groups;
   const int g = rem - hd * groups;
 
+  int64_t slot = -1;
+  if (cache) {
+    slot = p.slots[p.cu_seqlens != nullptr ? tok0 + n : (int64_t)b * p.N + n];
+    if (slot >= p.num_slots) slot = -1;
+  }
+  if (hd >= p.Hq + p.Hkv) {  // v head: copy into the cache
+    if (slot < 0) return;
+    const int h = hd - p.Hq - p.Hkv;
+    const int64_t vrow = p.cu_seqlens != nullptr ? (tok0 + n) * p.sv[2] : (int64_t)b * p.sv[0] + (int64_t)n * p.sv[2];
+    const T* vx = (const T*)p.v + vrow + (int64_t)h * p.sv[1];
+    T* dst = (T*)p.v_cache + slot * p.cs_slot + (int64_t)h * p.cs_head;
+    const int d1 = g * VEC, d2 = d1 + half;
+    *(V*)(dst + d1) = *(const V*)(vx + d1);
+    *(V*)(dst + d2) = *(const V*)(vx + d2);
+    return;
+  }
   const bool is_q = hd < p.Hq;
   const int h = is_q ? hd : hd - p.Hq;
   const int64_t* st = is_q ? p.sq : p.sk;
@@ -85,12 +106,17 @@ __global__ __launch_bounds__(256) void fa_rope_kernel(const RopeParams p) {
   }
   *(V*)(x + d1) = y1;
   *(V*)(x + d2) = y2;
+  if (!is_q && slot >= 0) {
+    T* dst = (T*)p.k_cache + slot * p.cs_slot + (int64_t)h * p.cs_head;
+    *(V*)(dst + d1) = y1;
+    *(V*)(dst + d2) = y2;
+  }
 }
 
 // Host entry used by the C ABI layer (arguments already validated).
 hipError_t rope_inplace(const RopeParams& p, int dtype, hipStream_t s) {
   const int vec = dtype == 0 ? 4 : 8;
-  const int64_t threads = (int64_t)p.N * (p.Hq + p.Hkv) * (p.D / 2 / vec);
+  const int64_t threads = (int64_t)p.N * (p.Hq + p.Hkv + (p.k_cache != nullptr ? p.Hkv : 0)) * (p.D / 2 / vec);
   if (threads == 0 || p.B == 0) return hipSuccess;
   const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)p.B);
   if (dtype == 0)

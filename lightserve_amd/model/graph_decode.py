@@ -147,9 +147,9 @@ class KVCacheDecoder:
         for i, layer in enumerate(self.w.layers):
             h, residual = add_norm(pending, residual, layer.input_layernorm_weight, cfg.rms_eps)
             q, k, v = matmul_shared_input(h, (layer.q_proj, layer.k_proj, layer.v_proj))
-            apply_rope_(q.view(B, nh, 1, hd), k.view(B, nkv, 1, hd), self.cos, self.sin, positions=pos)
-            self.k_cache[i].view(-1, nkv, hd).index_copy_(0, slot, k.view(B, nkv, hd))
-            self.v_cache[i].view(-1, nkv, hd).index_copy_(0, slot, v.view(B, nkv, hd))
+            # RoPE at each sequence's position; the rotated k and v rows go into the cache in the same launch
+            apply_rope_(q.view(B, nh, 1, hd), k.view(B, nkv, 1, hd), self.cos, self.sin, positions=pos,
+                        v=v.view(B, nkv, 1, hd), k_cache=self.k_cache[i], v_cache=self.v_cache[i], slots=slot)
             o = paged_attention_decode(q.view(B, nh, hd), self.k_cache[i], self.v_cache[i], self.block_tables,
                                        lens, max_seq_len=cfg.max_seq_len)
             h2, residual = fused_add_rmsnorm(matmul(o.view(B, nh * hd), layer.o_proj), residual,
@@ -186,9 +186,8 @@ class KVCacheDecoder:
                 k = matmul(h, layer.k_proj)
                 v = matmul(h, layer.v_proj)
                 apply_rope_(q.view(B, c, nh, hd).transpose(1, 2), k.view(B, c, nkv, hd).transpose(1, 2),
-                            self.cos, self.sin, positions=pos)
-                self.k_cache[i].view(-1, nkv, hd).index_copy_(0, slot, k.view(B * c, nkv, hd))
-                self.v_cache[i].view(-1, nkv, hd).index_copy_(0, slot, v.view(B * c, nkv, hd))
+                            self.cos, self.sin, positions=pos, v=v.view(B, c, nkv, hd).transpose(1, 2),
+                            k_cache=self.k_cache[i], v_cache=self.v_cache[i], slots=slot)
                 o = paged_prefill(q.view(B * c, nh, hd), self.k_cache[i], self.v_cache[i], self.block_tables, cu, lens,
                                   max_seqlen_q=c)
                 h2, residual = fused_add_rmsnorm(matmul(o.view(B * c, nh * hd), layer.o_proj), residual,

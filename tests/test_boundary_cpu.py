@@ -264,6 +264,20 @@ def test_abi_rope_validation(built_library):
     assert rc == -2 and "stride" in msg
     rc, msg = _lib.rope_check(_rope_args(max_pos=0))
     assert rc == -1 and "max_pos" in msg
+    # K/V cache append: v, both caches and slots together, aligned strides
+    cache = dict(v=1 << 20, k_cache=1 << 21, v_cache=1 << 22, slots=1 << 23, v_stride=_lib._i64x4(4096, 64, 256, 1),
+                 num_slots=64)
+    a = _rope_args(**cache)
+    a.cache_stride[0], a.cache_stride[1] = 4 * 64, 64
+    assert _lib.rope_check(a)[0] == 0
+    a = _rope_args(**{**cache, "slots": None})
+    a.cache_stride[0], a.cache_stride[1] = 4 * 64, 64
+    rc, msg = _lib.rope_check(a)
+    assert rc == -1 and "slots" in msg
+    a = _rope_args(**cache)
+    a.cache_stride[0], a.cache_stride[1] = 64, 64  # a slot must hold every head
+    rc, msg = _lib.rope_check(a)
+    assert rc == -2 and "caches" in msg
     # empty problems are a successful no-op; bad input never reaches the GPU
     _lib.rope(_rope_args(seqlen=0, q=None, k=None), 0)
     with pytest.raises(RuntimeError, match="LSFA_ERR_INVALID"):

@@ -56,6 +56,39 @@ def test_rope_kernel_matches_oracle(B, Hq, Hkv, N, D, packed, dtype, with_positi
     torch.testing.assert_close(k.double().cpu(), k_ref, atol=1e-5, rtol=1.01 * u)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,Hq,Hkv,N,D", [(3, 8, 2, 1, 128), (2, 4, 4, 37, 64)])
+def test_rope_appends_kv_to_cache(B, Hq, Hkv, N, D, dtype):
+    """The K/V cache append of apply_rope_ equals rotating then copying rows
+    with index_copy_ (bit for bit), skips negative slots, and leaves every
+    other slot of the caches untouched."""
+    print(f"case rope cache B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(B * N + D)
+    q = torch.randn(B, N, Hq, D, generator=g).to(dtype).cuda().transpose(1, 2)
+    k = torch.randn(B, N, Hkv, D, generator=g).to(dtype).cuda().transpose(1, 2)
+    v = torch.randn(B, N, Hkv, D, generator=g).to(dtype).cuda().transpose(1, 2)
+    cos, sin = om.precompute_rope(D, 512, 500000.0, dtype, "cuda")
+    pos = torch.tensor([11 * b + 2 for b in range(B)], dtype=torch.int32, device="cuda")
+    nblocks, bs = 64, 16
+    slots = torch.randperm(nblocks * bs, generator=g)[:B * N].cuda()
+    slots[1] = -1  # a padding token: not stored
+    kc = torch.full((nblocks, bs, Hkv, D), 7.0, dtype=dtype, device="cuda")
+    vc = torch.full_like(kc, 7.0)
+    q2, k2 = q.clone(), k.clone()
+    apply_rope_(q, k, cos, sin, positions=pos, v=v, k_cache=kc, v_cache=vc, slots=slots)
+    apply_rope_(q2, k2, cos, sin, positions=pos)  # the same rotation without the append
+    kr = torch.full_like(kc, 7.0)
+    vr = torch.full_like(vc, 7.0)
+    keep = slots >= 0
+    rows_k = k2.transpose(1, 2).reshape(B * N, Hkv, D)[keep]
+    rows_v = v.transpose(1, 2).reshape(B * N, Hkv, D)[keep]
+    kr.view(-1, Hkv, D).index_copy_(0, slots[keep], rows_k)
+    vr.view(-1, Hkv, D).index_copy_(0, slots[keep], rows_v)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q2) and torch.equal(k, k2)
+    assert torch.equal(kc, kr) and torch.equal(vc, vr)
+
+
 def test_rope_q_only_and_positions_clamped():
     """k = None rotates q alone; positions past the table clamp to its last row."""
     print("case rope q-only, clamp", flush=True)
