@@ -602,10 +602,11 @@ def bench_gemv(args):
     noise (algorithmic bytes = K*N*2 + M*K*2 + M*N*2). The timed loop calls the
     C ABI with prebuilt arguments. The sweep times every projection shape of
     the step at batch 1 and 8 (grouped where the decoder groups them) next to
-    torch.matmul (hipBLASLt)."""
+    torch.matmul (hipBLASLt); the skinny kernel is called directly, whatever
+    row count tiled_matmul.matmul would route to it."""
     import torch
     from lightserve_amd import _lib
-    from lightserve_amd.kernels.tiled_matmul import matmul_shared_input, skinny_matmul
+    from lightserve_amd.kernels.tiled_matmul import skinny_matmul, skinny_matmul_group
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -663,7 +664,7 @@ def bench_gemv(args):
         for name, k, ns in GEMV_SWEEP:
             a = torch.randn(rows, k, device=dev, generator=g).to(torch.bfloat16)
             ws_ = [(torch.randn(k, n, device=dev, generator=g) / k ** 0.5).to(torch.bfloat16) for n in ns]
-            t_lib = per_call_ms(lambda: matmul_shared_input(a, ws_))
+            t_lib = per_call_ms(lambda: skinny_matmul_group(a, ws_))
             t_blas = per_call_ms(lambda: [torch.matmul(a, b) for b in ws_])
             b = sum(k * n * 2 for n in ns)
             sweep.append({"proj": name, "m": rows, "k": k, "n": list(ns), "lsfa_ms": round(t_lib, 5),

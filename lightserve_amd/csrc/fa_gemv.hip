@@ -11,7 +11,11 @@
 //   of kc rows; thread (cg, kg) = (tid % 32, tid / 32) reads 16 bytes
 //   (8 columns) of rows kg, kg + 8, ... of the range, eight rows in flight, so
 //   each wave-load covers two 512-byte row segments, and keeps M x 8 fp32
-//   sums. x's K-range sits in LDS as fp32. The 8 K-groups are summed through
+//   sums. The products run on v_dot2_f32_{bf16,f16}: a thread's rows k and
+//   k + 8 (k % 16 < 8) are paired column by column with one v_perm_b32 per two
+//   columns, and x's K-range sits in LDS as the matching pairs
+//   (x[k], x[k + 8]), so two rows cost 8 permutes and 8 * M dot2 instead of
+//   16 conversions and 16 * M fp32 FMAs. The 8 K-groups are summed through
 //   LDS.
 //   With one split the workgroup rounds its sums into y. Otherwise it stores
 //   them as an fp32 partial block [split][M][256 columns] and counts its
@@ -59,6 +63,22 @@ __device__ __forceinline__ T* gemv_out(const GemvParams& p, int n, int m) {
   return y + (int64_t)m * sy + (n - col_off);
 }
 
+// acc + w.x * x.x + w.y * x.y for two packed bf16/fp16 pairs.
+__device__ __forceinline__ float gemv_dot2(uint32_t w, uint32_t x, float acc, __bf16*) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, x), acc, false);
+}
+__device__ __forceinline__ float gemv_dot2(uint32_t w, uint32_t x, float acc, _Float16*) {
+  typedef __fp16 half2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w), __builtin_bit_cast(half2_t, x), acc, false);
+}
+template <typename T>
+__device__ __forceinline__ uint32_t gemv_pack(T a, T b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+// Pair slots of a K-range of kc rows: pair (k, k + 8) with k % 16 < 8 sits at
+// (k / 16) * 8 + k % 8.
+__host__ __device__ constexpr int gemv_pair_slots(int kc) { return (kc + 15) / 16 * 8; }
+
 // M is the compile-time row capacity (1, 2, 4 or 8); p.M <= M rows are real.
 // Rows past p.M have x = 0 in LDS and their sums are not stored.
 template <typename T, int M>
@@ -94,25 +114,24 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
     wp += 8 * step;
   }
 
-  float* xs = gemv_smem;
-  if (p.xg == nullptr) {
-    for (int idx = tid; idx < M * k_len; idx += 256) {
-      const int m = idx / k_len, k = idx - m * k_len;
-      xs[m * p.kc + k] = m < p.M ? (float)((const T*)p.x)[(int64_t)m * p.sx + k_begin + k] : 0.f;
-    }
-  } else {
+  // x's K-range as (x[k], x[k + 8]) pairs in the input dtype; rows past the
+  // range and rows past p.M are zero.
+  uint32_t* xs = (uint32_t*)gemv_smem;
+  const int pslots = gemv_pair_slots(p.kc);
+  auto x_at = [&](int m, int k) -> T {
+    if (k >= k_len) return (T)0.f;
+    if (p.xg == nullptr) return ((const T*)p.x)[(int64_t)m * p.sx + k_begin + k];
     // SwiGLU input: silu(gate) rounded to T, times x rounded to T (the two
     // roundings of F.silu(gate) * up on bf16/fp16 tensors).
-    for (int idx = tid; idx < M * k_len; idx += 256) {
-      const int m = idx / k_len, k = idx - m * k_len;
-      float v = 0.f;
-      if (m < p.M) {
-        const float g = (float)((const T*)p.xg)[(int64_t)m * p.sxg + k_begin + k];
-        const float act = (float)(T)(g / (1.0f + expf(-g)));
-        v = (float)(T)(act * (float)((const T*)p.x)[(int64_t)m * p.sx + k_begin + k]);
-      }
-      xs[m * p.kc + k] = v;
-    }
+    const float g = (float)((const T*)p.xg)[(int64_t)m * p.sxg + k_begin + k];
+    const float act = (float)(T)(g / (1.0f + expf(-g)));
+    return (T)(act * (float)((const T*)p.x)[(int64_t)m * p.sx + k_begin + k]);
+  };
+  const int npairs = gemv_pair_slots(k_len);
+  for (int idx = tid; idx < M * npairs; idx += 256) {
+    const int m = idx / npairs, q = idx - m * npairs;
+    const int k0 = (q >> 3) * 16 + (q & 7);
+    xs[m * pslots + q] = m < p.M ? gemv_pack<T>(x_at(m, k0), x_at(m, k0 + 8)) : 0u;
   }
   __syncthreads();
 
@@ -122,15 +141,24 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[m][e] = 0.f;
 
-  auto fma_row = [&](const u32x4 raw, int k) {
-    const typename VecT<T>::x8 wv = __builtin_bit_cast(typename VecT<T>::x8, raw);
+  // Rows k (raw0) and k + 8 (raw1) of this thread's 8 columns, k % 16 < 8.
+  auto dot_rows = [&](const u32x4 raw0, const u32x4 raw1, int k) {
+    const int q = (k >> 4) * 8 + (k & 7);
+    uint32_t xv[M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float xv = xs[m * p.kc + k];
+    for (int m = 0; m < M; ++m) xv[m] = xs[m * pslots + q];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(xv, (float)wv[e], acc[m][e]);
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = __builtin_amdgcn_perm(raw1[e], raw0[e], 0x05040100u);  // column 2e of both rows
+      const uint32_t hi = __builtin_amdgcn_perm(raw1[e], raw0[e], 0x07060302u);  // column 2e + 1
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        acc[m][2 * e] = gemv_dot2(lo, xv[m], acc[m][2 * e], (T*)nullptr);
+        acc[m][2 * e + 1] = gemv_dot2(hi, xv[m], acc[m][2 * e + 1], (T*)nullptr);
+      }
     }
   };
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
   int k = kg;
   for (int b = 0; b < full; ++b) {
@@ -141,7 +169,7 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
       __builtin_amdgcn_sched_barrier(0);  // all eight loads issue before the first use
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) fma_row(cur[u], k + u * kGemvKG);
+    for (int u = 0; u < 8; u += 2) dot_rows(cur[u], cur[u + 1], k + u * kGemvKG);
     k += 8 * kGemvKG;
   }
   if (rem >= 4) {
@@ -150,15 +178,18 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
     for (int u = 0; u < 4; ++u) r4[u] = __builtin_nontemporal_load((const u32x4*)(wp + u * step));
     __builtin_amdgcn_sched_barrier(0);
     wp += 4 * step;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) fma_row(r4[u], k + u * kGemvKG);
+    dot_rows(r4[0], r4[1], k);
+    dot_rows(r4[2], r4[3], k + 2 * kGemvKG);
     k += 4 * kGemvKG;
   }
-  for (int u = 0; u < (rem & 3); ++u) {
-    fma_row(__builtin_nontemporal_load((const u32x4*)wp), k);
-    wp += step;
-    k += kGemvKG;
+  if ((rem & 3) >= 2) {
+    const u32x4 r0 = __builtin_nontemporal_load((const u32x4*)wp);
+    const u32x4 r1 = __builtin_nontemporal_load((const u32x4*)(wp + step));
+    wp += 2 * step;
+    dot_rows(r0, r1, k);
+    k += 2 * kGemvKG;
   }
+  if (rem & 1) dot_rows(__builtin_nontemporal_load((const u32x4*)wp), zero4, k);  // row k + 8 is past the range
 
   // Sum the K-groups: red[kg][m][column] over the x chunk.
   __syncthreads();  // every thread is done with xs
@@ -268,7 +299,7 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
 
 template <typename T, int M>
 static hipError_t launch_gemv_m(const GemvParams& p, hipStream_t s) {
-  const size_t xs_bytes = (size_t)M * p.kc * 4;
+  const size_t xs_bytes = (size_t)M * gemv_pair_slots(p.kc) * 4;
   const size_t red_bytes = (size_t)kGemvKG * M * kGemvCols * 4;
   const size_t lds = xs_bytes > red_bytes ? xs_bytes : red_bytes;
   const dim3 grid((unsigned)((p.N + kGemvCols - 1) / kGemvCols), (unsigned)p.splits);
