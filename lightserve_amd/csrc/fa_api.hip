@@ -450,7 +450,10 @@ int lsfa_prefill_paged(const lsfa_prefill_paged_args* a, void* stream) {
 }
 
 // Skinny GEMM split: about 1024 workgroups (256 columns x one K-range each)
-// with K-ranges of at least 64 rows (multiples of 8) and at most what keeps
+// with K-ranges of at least 128 rows (multiples of 8; measured on MI355X in
+// graph replays: 1024 workgroups with 128-row minimum beat 256-4096
+// workgroups and 32-256-row minimums on the decode projections, the narrow
+// ones gaining most from fewer splits) and at most what keeps
 // x's range within 32 KB of LDS at the kernel's row capacity (2048 rows up to
 // 4 rows, 1024 at 8). Workspace (only with more than one split): the int32
 // arrival counters, 16 per 256-column block, in a region of fixed size
@@ -466,7 +469,7 @@ GemvSplit gemv_split(long long M, long long K, long long N) {
   M = std::max(M, 0LL); K = std::max(K, 0LL); N = std::max(N, 0LL);
   const long long col_blocks = std::max(1LL, (N + 255) / 256);
   const long long kc_max = std::min(2048LL, 8192LL / lsfa::gemv_capacity((int)std::min(std::max(M, 1LL), 8LL)));
-  long long splits = std::max(1LL, std::min((1024 + col_blocks - 1) / col_blocks, (K + 63) / 64));
+  long long splits = std::max(1LL, std::min((1024 + col_blocks - 1) / col_blocks, (K + 127) / 128));
   long long kc = std::max(8LL, ((K + splits - 1) / splits + 7) / 8 * 8);
   kc = std::min(kc, kc_max);
   splits = std::max(1LL, (K + kc - 1) / kc);
