@@ -347,7 +347,16 @@ typedef struct {
  * x_gate (optional, NULL for none; [M, K] with row stride x_gate_stride):
  * the products read silu(x_gate) * x instead of x, each rounded to the dtype
  * as torch rounds F.silu(gate) * up (the SwiGLU input of a down projection,
- * model/minimal_llama.py's mlp). */
+ * model/minimal_llama.py's mlp).
+ * norm_weight (optional, NULL for none; [K]): the products read
+ * rmsnorm(x + residual) * norm_weight, computed exactly as lsfa_rmsnorm
+ * computes out (fp32 statistics; the reference's fused_add_rmsnorm,
+ * kernels/fused_rmsnorm_residual.py:30-70), so the norm before a projection
+ * needs no launch of its own. residual (optional, [M, K], row stride
+ * residual_stride) is added first; residual_out (optional, [M, K]) receives
+ * h = x + residual and must not overlap x or residual. Needs K % 8 == 0,
+ * 16-byte aligned rows and row strides that are multiples of 8 elements;
+ * excludes x_gate. */
 #define LSFA_GEMV_MAX_GROUP 4
 typedef struct {
   const void* x;
@@ -365,6 +374,13 @@ typedef struct {
   int32_t m;
   int32_t k;
   int32_t count;
+  const void* norm_weight;
+  const void* residual;
+  void* residual_out;
+  int64_t residual_stride;
+  int64_t residual_out_stride;
+  float eps;
+  int32_t reserved;
 } lsfa_gemv_group_args;
 
 /* Greedy next token of a decode step: tokens[r] = argmax over logits[r, :]

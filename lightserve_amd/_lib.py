@@ -124,6 +124,9 @@ class GemvGroupArgs(ctypes.Structure):
         ("w_stride", ctypes.c_int64 * GEMV_MAX_GROUP), ("y_stride", ctypes.c_int64 * GEMV_MAX_GROUP),
         ("n", ctypes.c_int32 * GEMV_MAX_GROUP),
         ("dtype", ctypes.c_int32), ("m", ctypes.c_int32), ("k", ctypes.c_int32), ("count", ctypes.c_int32),
+        ("norm_weight", ctypes.c_void_p), ("residual", ctypes.c_void_p), ("residual_out", ctypes.c_void_p),
+        ("residual_stride", ctypes.c_int64), ("residual_out_stride", ctypes.c_int64), ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
     ]
 
 

@@ -517,6 +517,32 @@ int lsfa_gemv_group_check(const lsfa_gemv_group_args* a) {
   if (!a->x) return fail(LSFA_ERR_INVALID, "x, w and y must be non-NULL");
   if (a->x_stride < a->k) return fail(LSFA_ERR_INVALID, "x_stride must be >= k");
   if (a->x_gate && a->x_gate_stride < a->k) return fail(LSFA_ERR_INVALID, "x_gate_stride must be >= k");
+  if (a->norm_weight) {
+    if (a->x_gate) return fail(LSFA_ERR_INVALID, "norm_weight and x_gate exclude each other");
+    if (!(a->eps >= 0.f) || !std::isfinite(a->eps)) return fail(LSFA_ERR_INVALID, "eps must be finite and >= 0");
+    if (a->k % 8 != 0 || a->x_stride % 8 != 0 || !aligned16(a->x) || !aligned16(a->norm_weight))
+      return fail(LSFA_ERR_UNSUPPORTED, "the fused RMSNorm needs k %% 8 == 0, x rows 16-byte aligned");
+    if (a->residual && (a->residual_stride < a->k || a->residual_stride % 8 != 0 || !aligned16(a->residual)))
+      return fail(LSFA_ERR_UNSUPPORTED, "residual rows must be 16-byte aligned with residual_stride >= k");
+    if (a->residual_out) {
+      if (a->residual_out_stride < a->k || a->residual_out_stride % 8 != 0 || !aligned16(a->residual_out))
+        return fail(LSFA_ERR_UNSUPPORTED, "residual_out rows must be 16-byte aligned with residual_out_stride >= k");
+      const int esz = 2;
+      auto span = [&](const void* base, int64_t stride) {
+        const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+        return std::make_pair(b, b + ((uint64_t)std::max(a->m - 1, 0) * stride + a->k) * esz);
+      };
+      const auto o = span(a->residual_out, a->residual_out_stride);
+      const auto xs = span(a->x, a->x_stride);
+      if (o.first < xs.second && xs.first < o.second)
+        return fail(LSFA_ERR_INVALID, "residual_out overlaps x (other workgroups still read it)");
+      if (a->residual) {
+        const auto rs = span(a->residual, a->residual_stride);
+        if (o.first < rs.second && rs.first < o.second)
+          return fail(LSFA_ERR_INVALID, "residual_out overlaps residual (other workgroups still read it)");
+      }
+    }
+  }
   for (int i = 0; i < a->count; ++i) {
     if (a->n[i] == 0) continue;
     if (!a->w[i] || !a->y[i]) return fail(LSFA_ERR_INVALID, "x, w and y must be non-NULL");
@@ -554,6 +580,12 @@ int lsfa_gemv_group(const lsfa_gemv_group_args* a, void* stream) {
   p.x = a->x;
   p.xg = a->x_gate;
   p.sxg = a->x_gate_stride;
+  p.nw = a->norm_weight;
+  p.nr = a->residual;
+  p.nh = a->residual_out;
+  p.snr = a->residual_stride;
+  p.snh = a->residual_out_stride;
+  p.eps = a->eps;
   int off = 0;
   for (int i = 0; i < 4; ++i) {
     p.col_off[i] = off;

@@ -206,6 +206,14 @@ struct GemvParams {
   int64_t sx;
   int M, K, N;
   int kc, splits;  // K-range per split and the number of splits
+  // Optional RMSNorm of the input (nw non-null): the products read
+  // rmsnorm(x + nr) * nw as fused_add_rmsnorm computes it; the workgroup
+  // (0, 0) writes h = x + nr to nh when nh is non-null.
+  const void* nw;
+  const void* nr;
+  void* nh;
+  int64_t snr, snh;
+  float eps;
 };
 
 // Which decode kernel serves a group size Hq/Hkv and block size 2^shift: the

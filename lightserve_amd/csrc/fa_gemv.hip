@@ -2,7 +2,9 @@
 // with W in the [in, out] row-major layout the model stores
 // (model/minimal_llama.py's weights), bf16/fp16 in, fp32 accumulate. Up to
 // four matrices that share x (a decoder's q/k/v or gate/up projections) run
-// as one launch over their concatenated columns.
+// as one launch over their concatenated columns. The input may be given as
+// the operands of a residual add + RMSNorm (the norm then needs no launch of
+// its own) or of SwiGLU.
 //
 // At M <= 8 the product is a pass over W (about M FLOP per weight byte), so it
 // is HBM-bound: the kernel is built to stream W once at full rate, in one
@@ -114,12 +116,63 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
     wp += 8 * step;
   }
 
+  // RMSNorm input: every workgroup forms the whole row's sum of squares of
+  // h = x + residual in the order of the vector RMSNorm kernel (256 threads,
+  // thread t adds columns (c * 256 + t) * 8 + e, then wave shuffles and the 4
+  // waves in order), so the scaled rows equal fused_add_rmsnorm's bit for bit
+  // where that kernel takes its vector path.
+  __shared__ float norm_red[8][4];
+  float rrms[M];
+  if (p.nw != nullptr) {
+    float ss[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      ss[m] = 0.f;
+      if (m < p.M) {
+        const T* xr = (const T*)p.x + (int64_t)m * p.sx;
+        const T* rr = p.nr != nullptr ? (const T*)p.nr + (int64_t)m * p.snr : nullptr;
+        T* hr = (p.nh != nullptr && blockIdx.x == 0 && blockIdx.y == 0) ? (T*)p.nh + (int64_t)m * p.snh : nullptr;
+        for (int col = tid * 8; col < p.K; col += 256 * 8) {
+          typename VecT<T>::x8 v = *(const typename VecT<T>::x8*)(xr + col);
+          if (rr != nullptr) {
+            const typename VecT<T>::x8 rv = *(const typename VecT<T>::x8*)(rr + col);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (T)((float)v[e] + (float)rv[e]);
+          }
+          if (hr != nullptr) *(typename VecT<T>::x8*)(hr + col) = v;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss[m] = fmaf((float)v[e], (float)v[e], ss[m]);
+        }
+      }
+#pragma unroll
+      for (int sh = 32; sh >= 1; sh >>= 1) ss[m] += __shfl_xor(ss[m], sh);
+      if ((tid & 63) == 0) norm_red[m][tid >> 6] = ss[m];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) t += norm_red[m][w];
+      rrms[m] = 1.f / sqrtf(t / (float)p.K + p.eps);
+    }
+  }
+
   // x's K-range as (x[k], x[k + 8]) pairs in the input dtype; rows past the
   // range and rows past p.M are zero.
   uint32_t* xs = (uint32_t*)gemv_smem;
   const int pslots = gemv_pair_slots(p.kc);
   auto x_at = [&](int m, int k) -> T {
     if (k >= k_len) return (T)0.f;
+    if (p.nw != nullptr) {
+      const int kk = k_begin + k;
+      T h = ((const T*)p.x)[(int64_t)m * p.sx + kk];
+      if (p.nr != nullptr) h = (T)((float)h + (float)((const T*)p.nr)[(int64_t)m * p.snr + kk]);
+      float r = 0.f;
+#pragma unroll
+      for (int i = 0; i < M; ++i) r = i == m ? rrms[i] : r;  // no dynamic register indexing
+      return (T)((float)h * r * (float)((const T*)p.nw)[kk]);
+    }
     if (p.xg == nullptr) return ((const T*)p.x)[(int64_t)m * p.sx + k_begin + k];
     // SwiGLU input: silu(gate) rounded to T, times x rounded to T (the two
     // roundings of F.silu(gate) * up on bf16/fp16 tensors).

@@ -21,6 +21,9 @@ routing stops at 2.
 Projections that share their input (a decoder's q/k/v, gate/up) go through
 matmul_shared_input, which runs them as one lsfa_gemv_group launch over their
 concatenated columns when they qualify for the skinny kernel.
+add_rmsnorm_matmul_shared_input also folds the residual add + RMSNorm that
+precedes such projections into that launch (the norm computed exactly as
+fused_add_rmsnorm computes it).
 
 lsfa_gemv's workspace carries arrival counters (its first
 LSFA_GEMV_COUNTER_BYTES) that must start at zero and that every call leaves
@@ -133,6 +136,53 @@ def swiglu_matmul(gate: torch.Tensor, up: torch.Tensor, b: torch.Tensor) -> torc
             and b.ndim == 2 and b.shape[0] == up.shape[1] and gate.stride(1) == 1 and _skinny_ok(up, b, AUTO_MAX_ROWS)):
         return skinny_matmul_group(up, [b], gate=gate)[0]
     return matmul(torch.nn.functional.silu(gate) * up, b)
+
+
+def _rows_addressable(t: torch.Tensor) -> bool:
+    return t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+
+
+def add_rmsnorm_matmul_shared_input(x, residual, weight, eps, bs, write_residual=True):
+    """(outs, h) for h = x + residual (x alone when residual is None) and
+    outs = [matmul(rmsnorm(h) * weight, b) for b in bs], the norm as
+    fused_add_rmsnorm computes it. Products of at most AUTO_MAX_ROWS rows run
+    as one skinny launch that also forms the norm (and writes h, when
+    write_residual and residual is given); others run fused_add_rmsnorm (or
+    rmsnorm) then matmul_shared_input. h is residual's replacement, as from
+    fused_add_rmsnorm, or x itself when residual is None."""
+    from .fused_rmsnorm_residual import fused_add_rmsnorm, rmsnorm
+    M, K = x.shape
+    fused = (len(bs) <= _lib.GEMV_MAX_GROUP and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
+             and K % 8 == 0 and _rows_addressable(x) and weight.is_contiguous() and weight.data_ptr() % 16 == 0
+             and weight.dtype == x.dtype and (residual is None or (residual.shape == x.shape and residual.dtype == x.dtype
+                                                                   and _rows_addressable(residual)))
+             and all(b.ndim == 2 and b.is_cuda and b.dtype == x.dtype and b.shape[0] == K
+                     and _skinny_ok(x, b, AUTO_MAX_ROWS) for b in bs))
+    if not fused:
+        normed, h = (fused_add_rmsnorm(x, residual, weight, eps) if residual is not None
+                     else (rmsnorm(x, weight, eps), x))
+        return matmul_shared_input(normed, bs), h
+    h = torch.empty_like(x) if (residual is not None and write_residual) else None
+    outs = [torch.empty(M, b.shape[1], dtype=x.dtype, device=x.device) for b in bs]
+    if M == 0:
+        return outs, (h if residual is not None else x)
+    args = _lib.GemvGroupArgs(x=x.data_ptr(), x_stride=x.stride(0), dtype=_lib.TORCH_TO_LSFA[x.dtype], m=M, k=K,
+                              count=len(bs), norm_weight=weight.data_ptr(), eps=float(eps))
+    if residual is not None:
+        args.residual, args.residual_stride = residual.data_ptr(), residual.stride(0)
+    if h is not None:
+        args.residual_out, args.residual_out_stride = h.data_ptr(), h.stride(0)
+    for i, (b, o) in enumerate(zip(bs, outs)):
+        args.w[i], args.y[i] = b.data_ptr(), o.data_ptr()
+        args.w_stride[i], args.y_stride[i], args.n[i] = b.stride(0), o.stride(0), b.shape[1]
+    nbytes = _lib.gemv_group_workspace_size(args)
+    with torch.cuda.device(x.device):
+        stream = _lib.current_stream(x.device)
+        if nbytes:
+            ws = _workspace(x.device, stream, nbytes)
+            args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+        _lib.gemv_group(args, stream)
+    return outs, (h if residual is not None else x)
 
 
 def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

@@ -33,7 +33,7 @@ from ..kernels.paged_attention import paged_attention_decode, paged_prefill
 from ..kernels.rope import apply_rope_
 from ..kernels.fused_rmsnorm_residual import fused_add_rmsnorm
 from ..kernels.greedy import greedy_next_token
-from ..kernels.tiled_matmul import matmul, matmul_shared_input, swiglu_matmul
+from ..kernels.tiled_matmul import add_rmsnorm_matmul_shared_input, matmul, swiglu_matmul
 from .minimal_llama import add_norm, init_weights, llama3_8b_shape, llama_forward, precompute_rope
 
 SEED_TOKEN_ID = 1
@@ -145,19 +145,22 @@ class KVCacheDecoder:
         residual = F.embedding(self.tokens, self.w.embed_tokens)  # [B, H]
         pending = None
         for i, layer in enumerate(self.w.layers):
-            h, residual = add_norm(pending, residual, layer.input_layernorm_weight, cfg.rms_eps)
-            q, k, v = matmul_shared_input(h, (layer.q_proj, layer.k_proj, layer.v_proj))
+            # residual add + RMSNorm folded into the q/k/v launch (the first layer's input is the embedding)
+            x_in, r_in = (residual, None) if pending is None else (pending, residual)
+            (q, k, v), residual = add_rmsnorm_matmul_shared_input(
+                x_in, r_in, layer.input_layernorm_weight, cfg.rms_eps, (layer.q_proj, layer.k_proj, layer.v_proj))
             # RoPE at each sequence's position; the rotated k and v rows go into the cache in the same launch
             apply_rope_(q.view(B, nh, 1, hd), k.view(B, nkv, 1, hd), self.cos, self.sin, positions=pos,
                         v=v.view(B, nkv, 1, hd), k_cache=self.k_cache[i], v_cache=self.v_cache[i], slots=slot)
             o = paged_attention_decode(q.view(B, nh, hd), self.k_cache[i], self.v_cache[i], self.block_tables,
                                        lens, max_seq_len=cfg.max_seq_len)
-            h2, residual = fused_add_rmsnorm(matmul(o.view(B, nh * hd), layer.o_proj), residual,
-                                             layer.post_attention_layernorm_weight, cfg.rms_eps)
-            gate, up = matmul_shared_input(h2, (layer.gate_proj, layer.up_proj))
+            (gate, up), residual = add_rmsnorm_matmul_shared_input(
+                matmul(o.view(B, nh * hd), layer.o_proj), residual, layer.post_attention_layernorm_weight,
+                cfg.rms_eps, (layer.gate_proj, layer.up_proj))
             pending = swiglu_matmul(gate, up, layer.down_proj)
-        final, _ = add_norm(pending, residual, self.w.norm_weight, cfg.rms_eps)
-        return matmul(final, self.w.lm_head)
+        (logits,), _ = add_rmsnorm_matmul_shared_input(pending, residual, self.w.norm_weight, cfg.rms_eps,
+                                                       (self.w.lm_head,), write_residual=False)
+        return logits
 
     def prefill(self, prompt, chunk_size):
         """Caches a prompt [B, P] chunk by chunk (the engine's chunked prefill:

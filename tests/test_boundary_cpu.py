@@ -476,6 +476,20 @@ def test_abi_gemv_group_validation(built_library):
     bad.y_stride[2] = 100
     rc, msg = _lib.gemv_group_check(bad)
     assert rc == -1 and "y_stride" in msg
+    # RMSNorm folded in: excludes x_gate; h must not overlap x or residual
+    norm = dict(norm_weight=1 << 23, residual=1 << 22, residual_stride=4096, residual_out=1 << 21,
+                residual_out_stride=4096, eps=1e-5)
+    assert _lib.gemv_group_check(_group_args(ns, **norm))[0] == 0
+    rc, msg = _lib.gemv_group_check(_group_args(ns, **{**norm, "x_gate": 8192, "x_gate_stride": 4096}))
+    assert rc == -1 and "exclude" in msg
+    rc, msg = _lib.gemv_group_check(_group_args(ns, **{**norm, "residual_out": 4096 + 64}))
+    assert rc == -1 and "overlaps x" in msg
+    rc, msg = _lib.gemv_group_check(_group_args(ns, **{**norm, "residual_out": 1 << 22}))
+    assert rc == -1 and "overlaps residual" in msg
+    rc, msg = _lib.gemv_group_check(_group_args(ns, **{**norm, "eps": float("nan")}))
+    assert rc == -1 and "eps" in msg
+    rc, msg = _lib.gemv_group_check(_group_args(ns, **{**norm, "k": 4092}))
+    assert rc != 0
     _lib.gemv_group(_group_args(ns, m=0, x=None), 0)  # empty: no-op
 
 

@@ -232,3 +232,36 @@ def test_swiglu_matmul(M):
         assert torch.equal(routed, fused)
     else:
         torch.testing.assert_close(routed.float(), (x.float() @ w.float()), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("M", [1, 2, 5])
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_rmsnorm_folded_into_skinny_matmul(M, with_residual):
+    """add_rmsnorm_matmul_shared_input: at M <= 2 one launch forms the norm
+    in the vector RMSNorm kernel's order and equals fused_add_rmsnorm (or
+    rmsnorm) followed by the same grouped skinny GEMM bit for bit, h
+    included; at M = 5 it falls back to those two calls."""
+    from lightserve_amd.kernels.tiled_matmul import add_rmsnorm_matmul_shared_input, skinny_matmul_group
+    print(f"case gemv rmsnorm M={M} residual={with_residual}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(20 + M)
+    H = 4096
+    x = torch.randn(M, H, device="cuda", generator=g).to(torch.bfloat16)
+    r = torch.randn(M, H, device="cuda", generator=g).to(torch.bfloat16) if with_residual else None
+    w_norm = (torch.rand(H, device="cuda", generator=g) + 0.5).to(torch.bfloat16)
+    ws = [(torch.randn(H, n, device="cuda", generator=g) / H ** 0.5).to(torch.bfloat16) for n in (4096, 1024, 1024)]
+    outs, h = add_rmsnorm_matmul_shared_input(x, r, w_norm, 1e-5, ws)
+    if r is not None:
+        normed, h_ref = fused_add_rmsnorm(x, r, w_norm, 1e-5)
+    else:
+        normed, h_ref = rmsnorm(x, w_norm, 1e-5), x
+    refs = skinny_matmul_group(normed, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h_ref)
+    for c, ref, w in zip(outs, refs, ws):
+        if M <= 2:
+            assert torch.equal(c, ref)
+        _assert_one_rounding(c, normed, w)
+    # without writing h the products are the same
+    outs2, _ = add_rmsnorm_matmul_shared_input(x, r, w_norm, 1e-5, ws, write_residual=False)
+    for c, c2 in zip(outs, outs2):
+        assert torch.equal(c, c2)
