@@ -206,7 +206,13 @@ typedef struct {
  * addressed as slots; cache_stride = elements between slots and between
  * heads, head-dim stride 1). t = b * seqlen + n, or the packed index with
  * cu_seqlens. Slots outside [0, num_slots) are skipped (a negative slot marks
- * a padding token). v has k's shape, v_stride its strides. */
+ * a padding token). v has k's shape, v_stride its strides. Instead of slots,
+ * block_tables (int32 [batch, max_blocks_per_seq], row stride
+ * block_table_stride) may name them: token n of sequence b at position
+ * p = positions[b] + n goes to block_tables[b, p / block_size] * block_size +
+ * p % block_size (the engine's paging, engine/block_manager.py:56-60);
+ * positions past the table or block ids outside [0, num_slots / block_size)
+ * are skipped. */
 typedef struct {
   void* q;
   void* k;
@@ -232,6 +238,10 @@ typedef struct {
   int64_t v_stride[4];
   int64_t cache_stride[2];
   int64_t num_slots;
+  const int32_t* block_tables;
+  int64_t block_table_stride;
+  int32_t block_size;
+  int32_t max_blocks_per_seq;
 } lsfa_rope_args;
 
 /* Fused residual add + RMSNorm over the rows of [rows, cols] matrices

@@ -154,7 +154,8 @@ class RopeArgs(ctypes.Structure):
         ("max_pos", ctypes.c_int32), ("reserved", ctypes.c_int32),
         ("v", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
         ("slots", ctypes.c_void_p), ("v_stride", _i64x4), ("cache_stride", ctypes.c_int64 * 2),
-        ("num_slots", ctypes.c_int64),
+        ("num_slots", ctypes.c_int64), ("block_tables", ctypes.c_void_p), ("block_table_stride", ctypes.c_int64),
+        ("block_size", ctypes.c_int32), ("max_blocks_per_seq", ctypes.c_int32),
     ]
 
 

@@ -683,8 +683,12 @@ int lsfa_rope_check(const lsfa_rope_args* a) {
     if (!aligned16(ptr)) return fail(LSFA_ERR_UNSUPPORTED, "%s: base pointer is not 16-byte aligned", name);
   }
   if (a->k_cache != nullptr) {
-    if (a->heads_kv == 0 || !a->v || !a->v_cache || !a->slots)
-      return fail(LSFA_ERR_INVALID, "a K/V cache append needs heads_kv > 0 and non-NULL v, v_cache and slots");
+    if (a->heads_kv == 0 || !a->v || !a->v_cache || (!a->slots && !a->block_tables))
+      return fail(LSFA_ERR_INVALID, "a K/V cache append needs heads_kv > 0, non-NULL v and v_cache, and slots "
+                  "or block_tables");
+    if (a->block_tables && (a->block_size <= 0 || a->max_blocks_per_seq < 0 ||
+                            a->block_table_stride < a->max_blocks_per_seq))
+      return fail(LSFA_ERR_INVALID, "block_tables needs block_size > 0 and block_table_stride >= max_blocks_per_seq");
     if (a->num_slots < 0) return fail(LSFA_ERR_INVALID, "num_slots must be >= 0");
     if (a->v_stride[3] != 1 || !aligned16(a->v))
       return fail(LSFA_ERR_UNSUPPORTED, "v: head-dim stride must be 1 and the pointer 16-byte aligned");
@@ -719,6 +723,8 @@ int lsfa_rope(const lsfa_rope_args* a, void* stream) {
     p.v = a->v; p.k_cache = a->k_cache; p.v_cache = a->v_cache; p.slots = a->slots;
     for (int i = 0; i < 4; ++i) p.sv[i] = a->v_stride[i];
     p.cs_slot = a->cache_stride[0]; p.cs_head = a->cache_stride[1]; p.num_slots = a->num_slots;
+    p.block_tables = a->block_tables; p.sbt = a->block_table_stride;
+    p.block_size = a->block_size; p.max_blocks = a->max_blocks_per_seq;
   }
   hipError_t e = lsfa::rope_inplace(p, a->dtype, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "rope launch failed: %s", hipGetErrorString(e));

@@ -269,6 +269,9 @@ struct RopeParams {
   const int64_t* slots;
   int64_t sv[4];
   int64_t cs_slot, cs_head, num_slots;
+  const int32_t* block_tables;  // or slots from the block table and the token's position
+  int64_t sbt;
+  int block_size, max_blocks;
 };
 
 // Fused residual add + RMSNorm over rows of a [rows, cols] matrix (column

@@ -67,7 +67,16 @@ __global__ __launch_bounds__(256) void fa_rope_kernel(const RopeParams p) {
 
   int64_t slot = -1;
   if (cache) {
-    slot = p.slots[p.cu_seqlens != nullptr ? tok0 + n : (int64_t)b * p.N + n];
+    if (p.block_tables != nullptr) {
+      const int tp = (p.pos0 != nullptr ? p.pos0[b] : 0) + n;
+      const int bi = tp >= 0 ? tp / p.block_size : -1;
+      if (bi >= 0 && bi < p.max_blocks) {
+        const int64_t blk = p.block_tables[(int64_t)b * p.sbt + bi];
+        if (blk >= 0) slot = blk * p.block_size + (tp - bi * p.block_size);
+      }
+    } else {
+      slot = p.slots[p.cu_seqlens != nullptr ? tok0 + n : (int64_t)b * p.N + n];
+    }
     if (slot >= p.num_slots) slot = -1;
   }
   if (hd >= p.Hq + p.Hkv) {  // v head: copy into the cache

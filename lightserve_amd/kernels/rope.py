@@ -44,23 +44,32 @@ def _addressable(t):
     return t.stride(-1) == 1 and all((s * elem) % 16 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
 
 
-def apply_rope_(q, k, cos, sin, positions=None, *, v=None, k_cache=None, v_cache=None, slots=None):
+def apply_rope_(q, k, cos, sin, positions=None, *, v=None, k_cache=None, v_cache=None, slots=None,
+                block_tables=None):
     """Rotates q and k (None: q only) in place and returns them. With
     k_cache/v_cache ([num_blocks, block_size, heads_kv, head_dim]), v (k's
     shape) and slots (int64 [batch * seqlen], token b*seqlen+n -> cache slot
-    block * block_size + offset; negative: not stored), the rotated k rows and
-    v's rows are also written into the caches by the same launch."""
+    block * block_size + offset; negative: not stored) or block_tables (int32
+    [batch, max_blocks]: the slot of token n of sequence b follows from its
+    position positions[b] + n), the rotated k rows and v's rows are also
+    written into the caches by the same launch."""
     _check(q, k, cos, sin)
     if k_cache is not None:
-        assert k is not None and v is not None and v_cache is not None and slots is not None, (
-            "a cache append needs k, v, k_cache, v_cache and slots")
+        assert k is not None and v is not None and v_cache is not None, (
+            "a cache append needs k, v, k_cache, v_cache and slots or block_tables")
         assert v.shape == k.shape and v.dtype == k.dtype and _addressable(v), "v must match k and be addressable"
         assert k_cache.shape == v_cache.shape and k_cache.dim() == 4 and k_cache.dtype == k.dtype, (
             "k_cache and v_cache must be [num_blocks, block_size, heads_kv, head_dim] in k's dtype")
         assert k_cache.shape[2:] == (k.shape[1], k.shape[3]), "cache heads / head_dim differ from k"
         assert k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous"
-        assert slots.dtype == torch.int64 and slots.is_cuda and slots.numel() == k.shape[0] * k.shape[2], (
-            "slots must be an int64 GPU tensor with one entry per token")
+        assert (slots is None) != (block_tables is None), "give either slots or block_tables"
+        if slots is not None:
+            assert slots.dtype == torch.int64 and slots.is_cuda and slots.numel() == k.shape[0] * k.shape[2], (
+                "slots must be an int64 GPU tensor with one entry per token")
+        else:
+            assert block_tables.dtype == torch.int32 and block_tables.is_cuda and block_tables.dim() == 2 and \
+                block_tables.shape[0] == k.shape[0] and block_tables.stride(1) == 1, (
+                    "block_tables must be an int32 GPU tensor [batch, max_blocks] with unit column stride")
     assert _addressable(q) and (k is None or _addressable(k)), \
         "apply_rope_ needs unit head-dim stride and 16-byte aligned strides (use apply_rope for other layouts)"
     B, Hq, N, D = q.shape
@@ -77,9 +86,13 @@ def apply_rope_(q, k, cos, sin, positions=None, *, v=None, k_cache=None, v_cache
         heads_kv=k.shape[1] if k is not None else 0, head_dim=D, max_pos=c.shape[0], reserved=0,
     )
     if k_cache is not None:
-        sl = slots.contiguous()
-        args.v, args.k_cache, args.v_cache, args.slots = v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), \
-            sl.data_ptr()
+        sl = slots.contiguous() if slots is not None else None
+        args.v, args.k_cache, args.v_cache = v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr()
+        if sl is not None:
+            args.slots = sl.data_ptr()
+        else:
+            args.block_tables, args.block_table_stride = block_tables.data_ptr(), block_tables.stride(0)
+            args.block_size, args.max_blocks_per_seq = k_cache.shape[1], block_tables.shape[1]
         args.v_stride = _lib.strides4(v)
         args.cache_stride[0], args.cache_stride[1] = k_cache.stride(1), k_cache.stride(2)
         args.num_slots = k_cache.shape[0] * k_cache.shape[1]

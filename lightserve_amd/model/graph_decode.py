@@ -139,8 +139,6 @@ class KVCacheDecoder:
         cfg, B = self.cfg, self.B
         nh, nkv, hd = cfg.n_heads, cfg.kv_heads, cfg.head_dim
         pos = self.seq_lens
-        slot = self.block_tables.gather(1, (pos // self.bs).long().unsqueeze(1)).squeeze(1).long() * self.bs \
-            + (pos % self.bs).long()
         lens = pos + 1
         residual = F.embedding(self.tokens, self.w.embed_tokens)  # [B, H]
         pending = None
@@ -149,9 +147,11 @@ class KVCacheDecoder:
             x_in, r_in = (residual, None) if pending is None else (pending, residual)
             (q, k, v), residual = add_rmsnorm_matmul_shared_input(
                 x_in, r_in, layer.input_layernorm_weight, cfg.rms_eps, (layer.q_proj, layer.k_proj, layer.v_proj))
-            # RoPE at each sequence's position; the rotated k and v rows go into the cache in the same launch
+            # RoPE at each sequence's position; the same launch stores the rotated k and v rows at the slot
+            # its block table gives for that position
             apply_rope_(q.view(B, nh, 1, hd), k.view(B, nkv, 1, hd), self.cos, self.sin, positions=pos,
-                        v=v.view(B, nkv, 1, hd), k_cache=self.k_cache[i], v_cache=self.v_cache[i], slots=slot)
+                        v=v.view(B, nkv, 1, hd), k_cache=self.k_cache[i], v_cache=self.v_cache[i],
+                        block_tables=self.block_tables)
             o = paged_attention_decode(q.view(B, nh, hd), self.k_cache[i], self.v_cache[i], self.block_tables,
                                        lens, max_seq_len=cfg.max_seq_len)
             (gate, up), residual = add_rmsnorm_matmul_shared_input(

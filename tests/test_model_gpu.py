@@ -87,6 +87,25 @@ def test_rope_appends_kv_to_cache(B, Hq, Hkv, N, D, dtype):
     torch.cuda.synchronize()
     assert torch.equal(q, q2) and torch.equal(k, k2)
     assert torch.equal(kc, kr) and torch.equal(vc, vr)
+    # the same slots named by a block table and the positions instead
+    nb_seq = (11 * (B - 1) + 2 + N + bs - 1) // bs + 1
+    table = torch.randperm(nblocks, generator=g)[:B * nb_seq].view(B, nb_seq).to(torch.int32)
+    table[0, 0] = -1  # a block id outside the cache: that token is not stored
+    tp = torch.tensor([[11 * b + 2 + n for n in range(N)] for b in range(B)])
+    tslots = (table.long().gather(1, tp // bs) * bs + tp % bs).view(-1)
+    tslots[tslots < 0] = -1
+    kc2 = torch.full_like(kc, 7.0)
+    vc2 = torch.full_like(vc, 7.0)
+    q3, k3 = q2.clone(), k.clone()  # rotate the unrotated inputs again
+    q3.copy_(torch.randn(B, N, Hq, D, generator=g).to(dtype).cuda().transpose(1, 2))
+    k3 = torch.randn(B, N, Hkv, D, generator=g).to(dtype).cuda().transpose(1, 2)
+    q4, k4 = q3.clone(), k3.clone()
+    kc3, vc3 = torch.full_like(kc, 7.0), torch.full_like(vc, 7.0)
+    apply_rope_(q3, k3, cos, sin, positions=pos, v=v, k_cache=kc2, v_cache=vc2, block_tables=table.cuda())
+    apply_rope_(q4, k4, cos, sin, positions=pos, v=v, k_cache=kc3, v_cache=vc3, slots=tslots.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(q3, q4) and torch.equal(k3, k4)
+    assert torch.equal(kc2, kc3) and torch.equal(vc2, vc3)
 
 
 def test_rope_q_only_and_positions_clamped():
