@@ -848,6 +848,23 @@ def main():
         "roofline": roofline,
     }
     if bwd is not None:
+        # The reference's forward benchmark times the inference entry point
+        # (kernels/benchmark_flash_attention.py: flash_attention_forward, no
+        # logsumexp); timed here the same way, back to back over --steps calls.
+        from lightserve_amd.kernels.flash_attention import flash_attention_forward
+        for _ in range(2):
+            flash_attention_forward(q, k, v, causal=inp["causal"])
+        fi0, fi1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        fi0.record(stream)
+        for _ in range(args.steps):
+            flash_attention_forward(q, k, v, causal=inp["causal"])
+        fi1.record(stream)
+        torch.cuda.synchronize()
+        fi_ms = fi0.elapsed_time(fi1) / args.steps
+        result["fwd_inference"] = {"tflops": round(f_fwd / (fi_ms * 1e-3) / 1e12, 2), "ms": round(fi_ms, 5),
+                                   "pct_of_peak": round(100 * f_fwd / (fi_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                                   "entry": "flash_attention_forward (no logsumexp), back to back"}
         bwd_avg = sum(bwd_ms) / len(bwd_ms)
         fb = bwd_flops(*q.shape, inp["causal"])
         result["bwd"] = {"tflops": round(fb / (bwd_avg * 1e-3) / 1e12, 2), "ms": round(bwd_avg, 5),
