@@ -64,10 +64,14 @@ def skinny_matmul(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor = None) ->
     """C = A @ B for a [M <= 8, K], b [K, N] (bf16/fp16, N % 8 == 0, rows of
     b 16-byte aligned) through lsfa_gemv; fp32 accumulation, one rounding."""
     assert _skinny_ok(a, b), "skinny_matmul needs M <= 8, bf16/fp16, unit column strides, N % 8 == 0"
+    assert a.shape[1] == b.shape[0] and a.dtype == b.dtype and a.is_cuda and b.is_cuda, (
+        "a [M, K] and b [K, N] must share K, dtype and device")
     M, K = a.shape
     N = b.shape[1]
     if out is None:
         out = torch.empty(M, N, dtype=a.dtype, device=a.device)
+    assert out.shape == (M, N) and out.dtype == a.dtype and out.is_cuda and out.stride(1) == 1, (
+        "out must be [M, N] in a's dtype with unit column stride")
     if M == 0 or N == 0:
         return out
     if K == 0:
@@ -96,8 +100,12 @@ def skinny_matmul_group(a: torch.Tensor, bs, outs=None, gate: torch.Tensor = Non
     assert all(_skinny_ok(a, b) and b.shape[0] == a.shape[1] and b.dtype == a.dtype for b in bs), (
         "every matrix must qualify for skinny_matmul with the shared input")
     M, K = a.shape
+    assert a.is_cuda and all(b.is_cuda for b in bs), "GPU tensors expected"
     if outs is None:
         outs = [torch.empty(M, b.shape[1], dtype=a.dtype, device=a.device) for b in bs]
+    assert len(outs) == len(bs) and all(
+        o.shape == (M, b.shape[1]) and o.dtype == a.dtype and o.is_cuda and o.stride(1) == 1 for o, b in zip(outs, bs)), (
+        "outs must be [M, N_i] in a's dtype with unit column stride")
     if M == 0 or sum(b.shape[1] for b in bs) == 0:
         return outs
     if K == 0:
@@ -151,6 +159,7 @@ def add_rmsnorm_matmul_shared_input(x, residual, weight, eps, bs, write_residual
     rmsnorm) then matmul_shared_input. h is residual's replacement, as from
     fused_add_rmsnorm, or x itself when residual is None."""
     from .fused_rmsnorm_residual import fused_add_rmsnorm, rmsnorm
+    assert x.ndim == 2 and weight.ndim == 1 and weight.shape[0] == x.shape[1], "x [M, K] and weight [K] expected"
     M, K = x.shape
     fused = (len(bs) <= _lib.GEMV_MAX_GROUP and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
              and K % 8 == 0 and _rows_addressable(x) and weight.is_contiguous() and weight.data_ptr() % 16 == 0

@@ -505,6 +505,20 @@ def test_abi_greedy_validation(built_library):
     _lib.greedy(_lib.GreedyArgs(**{**base, "rows": 0, "logits": None}), 0)  # empty: no-op
 
 
+def test_skinny_matmul_argument_checks_cpu():
+    """Shape checks of the skinny GEMM's Python entry points run before any
+    library call (CPU tensors reach the assertions first)."""
+    from lightserve_amd.kernels.tiled_matmul import add_rmsnorm_matmul_shared_input, skinny_matmul, skinny_matmul_group
+    a = torch.randn(2, 16).to(torch.bfloat16)
+    b = torch.randn(16, 8).to(torch.bfloat16)
+    with pytest.raises(AssertionError):
+        skinny_matmul(a, b)  # CPU tensors
+    with pytest.raises(AssertionError):
+        skinny_matmul_group(a, [b])
+    with pytest.raises(AssertionError):
+        add_rmsnorm_matmul_shared_input(a, None, torch.randn(15).to(torch.bfloat16), 1e-6, [b])
+
+
 def test_rmsnorm_and_matmul_validation_cpu():
     """The reference's argument checks, in its order, raise AssertionError on
     CPU tensors before any library call (kernels/tests/test_fused_rmsnorm_residual.py,
