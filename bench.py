@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3] [--no-cpu-baseline]
 
 A step is one pass of the training hot path over one batch of synthetic
-input: forward with logsumexp, then backward (dQ, dK, dV), on BASELINE
+input: forward with logsumexp, then backward (dQ, dK, dV), on the benchmark
 config 3 (causal bf16, B=4, H=32, N=4096, D=128, q/k/v ~ N(0,1)*0.5, dO ~
 N(0,1), seed 2) by default; --config 2/4/5 time the other configurations
 (forward only for 2 and 5). Inputs are resident in HBM before the timed
@@ -48,7 +48,7 @@ def parse_args():
     ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
     ap.add_argument("--workload", default="attention",
                     choices=["attention", "decode", "prefill", "rope", "rmsnorm", "gemv"],
-                    help="attention: a BASELINE config (default); decode: a paged-KV decode step; "
+                    help="attention: a benchmark config 2-5 (default 3); decode: a paged-KV decode step; "
                          "prefill: config 5's chunks over a paged KV cache; "
                          "rope: in-place RoPE of config 3's q and k projections; "
                          "rmsnorm: fused residual add + RMSNorm, [2048, 8192] bf16")
@@ -335,7 +335,7 @@ def bench_rope(args):
 
 
 def bench_prefill(args):
-    """Chunked prefill over a paged KV cache (lsfa_prefill_paged): BASELINE
+    """Chunked prefill over a paged KV cache (lsfa_prefill_paged): benchmark
     config 5's workload (B=8, Hq=32, Hkv=8, D=128, a 512-token chunk after a
     prefix of 1024..8192 tokens per sequence, bf16, seed 4) with each
     sequence's K/V in a cache of 16-token blocks handed out in a shuffled

@@ -1,6 +1,6 @@
 """Error gates shared by the GPU parity tests.
 
-BASELINE correctness gate for fp16/bf16 outputs vs an fp32/fp64 eager oracle
+The correctness gate (max-abs 2e-2, mean-abs 2e-3; logsumexp 1e-3) for fp16/bf16 outputs vs an fp32/fp64 eager oracle
 on the same (cast) inputs: max-abs <= 2e-2 and mean-abs <= 2e-3; logsumexp
 max-abs <= 1e-3. The same max/mean gate is applied to dQ/dK/dV.
 """
@@ -25,7 +25,7 @@ def assert_gate(got, ref, what, max_abs=MAX_ABS, mean_abs=MEAN_ABS):
 
 
 def assert_grad_parity(got, exact, ref_alg, what, slack=1.5):
-    """Gradient check. Passes the BASELINE gate outright, or else must be no
+    """Gradient check. Passes the max-abs / mean-abs gate outright, or else must be no
     worse than `slack` x the error of the reference's own algorithm (the
     restated tiled backward with the reference's bf16 rounding points, outputs
     stored in the input dtype) against the same exact gradients. Also prints

@@ -2,7 +2,7 @@
 
 Mirrors the reference's forward tests (kernels/tests/test_flash_attention.py:
 shapes :24-31, dtypes and tolerances :40-61, non-contiguous input :65-77)
-with the oracle in place of SDPA, adds fp16, logsumexp, the BASELINE gate at
+with the oracle in place of SDPA, adds fp16, logsumexp, the correctness gate (max-abs 2e-2, mean-abs 2e-3, LSE 1e-3) at
 the full config sizes, head dims that need padding, graph capture and a
 side stream.
 """
@@ -118,7 +118,7 @@ def test_config1_against_golden(gpu):
 
 @pytest.mark.parametrize("cfg", [2, 3, 4])
 def test_config_forward_full_size(gpu, cfg):
-    """BASELINE gate at the full config size (oracle in fp32 on the GPU;
+    """The max-abs / mean-abs / LSE gate at the full config size (oracle in fp32 on the GPU;
     config 4 checks 4 of its 16 heads to bound the oracle's time)."""
     print(f"case config {cfg} forward full size", flush=True)
     inp = make_config_inputs(cfg, device=gpu)

@@ -3,7 +3,7 @@
 The reference has no decode kernel (its engine documents it as missing,
 engine/README.md "No decode-shaped attention kernel"), so parity is against
 oracle.attention.paged_decode_reference (gather through the block table,
-then the closed-form attention), under the BASELINE gate (max-abs 2e-2,
+then the closed-form attention), under the correctness gate (max-abs 2e-2,
 mean-abs 2e-3, lse 1e-3). Two kernels are covered: the MFMA kernel (block
 sizes that are multiples of 16, any group size up to 32) and the lane-group
 kernel (smaller blocks, groups 1/2/4/8). Cases: GQA group sizes 1-32, head

@@ -5,12 +5,12 @@ one scheduled token as the missing path (engine/request.py:86-93,
 engine/scheduler.py:34-44). Parity is against
 oracle.attention.paged_prefill_reference (gather through the block table, then
 the closed-form attention with the bottom-right causal mask) under the
-BASELINE gate, and, where the cache holds the same K/V as a packed layout,
+correctness gate (max-abs 2e-2, mean-abs 2e-3, LSE 1e-3), and, where the cache holds the same K/V as a packed layout,
 against the packed varlen forward bit for bit (the paged loads fill the same
 LDS tiles). Cases: GQA groups 1/3/4/8, head dims 64/96/128, block sizes
 16/32/64, ragged and empty chunks and sequences, single-token chunks, shuffled
 physical blocks, the device-side clamp of seq_lens_k, chunk-by-chunk prefill
-against one causal pass, and the BASELINE config-5 shape.
+against one causal pass, and the config-5 shape (B=8, Hq=32, Hkv=8, D=128, 512-token chunks).
 """
 import pytest
 import torch
@@ -125,7 +125,7 @@ def test_prefill_seq_lens_clamped_on_device(gpu):
 
 
 def test_prefill_config5_shape(gpu):
-    """BASELINE config 5 (B=8, Hq=32, Hkv=8, D=128, 512-token chunks after
+    """Config 5 (B=8, Hq=32, Hkv=8, D=128, 512-token chunks after
     prefixes of 1024..8192 tokens) with K/V in a shuffled 16-token-block cache:
     bit-identical to the packed varlen forward, and one sequence's first and
     last heads against the oracle."""
