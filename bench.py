@@ -660,7 +660,7 @@ def bench_gemv(args):
         return s.elapsed_time(e) / iters
 
     sweep = []
-    for rows in ([] if args.no_sweep else (1, 2, 3, 4, 8)):
+    for rows in ([] if args.no_sweep else (1, 2, 3, 4, 8, 16, 32)):
         for name, k, ns in GEMV_SWEEP:
             a = torch.randn(rows, k, device=dev, generator=g).to(torch.bfloat16)
             ws_ = [(torch.randn(k, n, device=dev, generator=g) / k ** 0.5).to(torch.bfloat16) for n in ns]

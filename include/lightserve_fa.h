@@ -318,7 +318,9 @@ typedef struct {
 } lsfa_prefill_paged_args;
 
 /* Skinny GEMM for decode-time projections: y[M, N] = x[M, K] @ w[K, N] with
- * M <= 8, w in the reference model's [in, out] row-major weight layout
+ * M <= 8 (up to 32 when every width is a multiple of 128, x rows are 16-byte
+ * aligned and the input is plain x: those run on MFMA), w in the reference
+ * model's [in, out] row-major weight layout
  * (model/minimal_llama.py: every Linear is x @ w), bf16 or fp16, fp32
  * accumulate, one rounding. The reference calls its tiled GEMM for these
  * (kernels/tiled_matmul.py:135-164, through model/minimal_llama.py:178-182);

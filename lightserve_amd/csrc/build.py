@@ -17,7 +17,7 @@ PKG = os.path.dirname(HERE)
 REPO = os.path.dirname(PKG)
 OUT = os.path.join(PKG, "liblsfa_gfx950.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_f32.hip", "fa_decode.hip", "fa_rope.hip", "fa_norm.hip", "fa_gemv.hip", "fa_sample.hip", "fa_api.hip"]
+SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_f32.hip", "fa_decode.hip", "fa_rope.hip", "fa_norm.hip", "fa_gemv.hip", "fa_gemv_mfma.hip", "fa_sample.hip", "fa_api.hip"]
 HEADERS = ["fa_common.hpp", os.path.join("..", "..", "include", "lightserve_fa.h")]
 
 ARCH = "gfx950"

@@ -20,6 +20,7 @@ hipError_t decode_gqa(const DecodeParams& p, bool is_bf16, int dp, hipStream_t s
 hipError_t rope_inplace(const RopeParams& p, int dtype, hipStream_t s);
 hipError_t add_rmsnorm(const NormParams& p, int dtype, bool vec, hipStream_t s);
 hipError_t gemv(const GemvParams& p, bool is_bf16, hipStream_t s);
+hipError_t gemv_mfma(const GemvParams& p, bool is_bf16, hipStream_t s);
 int gemv_capacity(int m);
 hipError_t greedy(const void* logits, int64_t stride, int dtype, int rows, int cols, int64_t* tokens,
                   int32_t* seq_lens, hipStream_t s);
@@ -464,6 +465,33 @@ struct GemvSplit {
   uint64_t counter_bytes = 0, bytes = 0;
 };
 
+// The MFMA kernel (fa_gemv_mfma.hip) serves 3..32 rows when every matrix's
+// width is a multiple of 128 and the input is plain x: K-ranges of at most 256
+// rows (four 64-row tiles per workgroup), 128-column blocks.
+bool gemv_uses_mfma(const lsfa_gemv_group_args* a) {
+  if (a->m < 3 || a->m > 32 || a->x_gate || a->norm_weight || a->k % 8 != 0 || a->x_stride % 8 != 0 ||
+      !aligned16(a->x))
+    return false;
+  long long n = 0;
+  for (int i = 0; i < a->count; ++i) {
+    if (a->n[i] % 128 != 0) return false;
+    n += a->n[i];
+  }
+  return n / 128 <= LSFA_GEMV_COUNTER_BYTES / 64;
+}
+
+GemvSplit gemv_split_mfma(long long M, long long K, long long N) {
+  GemvSplit g;
+  M = std::max(M, 0LL); K = std::max(K, 0LL); N = std::max(N, 0LL);
+  g.kc = (int)std::min(256LL, std::max(64LL, (K + 63) / 64 * 64));
+  g.splits = (int)std::max(1LL, (K + g.kc - 1) / g.kc);
+  if (g.splits > 1) {
+    g.counter_bytes = LSFA_GEMV_COUNTER_BYTES;
+    g.bytes = g.counter_bytes + align256((uint64_t)g.splits * M * N * 4);
+  }
+  return g;
+}
+
 GemvSplit gemv_split(long long M, long long K, long long N) {
   GemvSplit g;
   M = std::max(M, 0LL); K = std::max(K, 0LL); N = std::max(N, 0LL);
@@ -505,7 +533,9 @@ int lsfa_gemv_group_check(const lsfa_gemv_group_args* a) {
   if (a->count < 1 || a->count > LSFA_GEMV_MAX_GROUP)
     return fail(LSFA_ERR_INVALID, "count must be 1..%d (count=%d)", LSFA_GEMV_MAX_GROUP, a->count);
   if (a->m < 0 || a->k < 0) return fail(LSFA_ERR_INVALID, "negative size (m=%d k=%d)", a->m, a->k);
-  if (a->m > 8) return fail(LSFA_ERR_UNSUPPORTED, "gemv takes at most 8 rows (m=%d)", a->m);
+  if (a->m > 8 && !gemv_uses_mfma(a))
+    return fail(LSFA_ERR_UNSUPPORTED, "gemv takes at most 8 rows, or 32 with plain x, widths that are multiples of "
+                "128 and 16-byte aligned x rows (m=%d)", a->m);
   for (int i = 0; i < a->count; ++i) {
     if (a->n[i] < 0) return fail(LSFA_ERR_INVALID, "negative size (n=%d)", a->n[i]);
     if (a->n[i] % 8 != 0) return fail(LSFA_ERR_UNSUPPORTED, "gemv needs n %% 8 == 0 (n=%d)", a->n[i]);
@@ -550,7 +580,7 @@ int lsfa_gemv_group_check(const lsfa_gemv_group_args* a) {
       return fail(LSFA_ERR_UNSUPPORTED, "w rows must be 16-byte aligned with w_stride >= n and a multiple of 8");
     if (a->y_stride[i] < a->n[i]) return fail(LSFA_ERR_INVALID, "y_stride must be >= n");
   }
-  const GemvSplit g = gemv_split(a->m, a->k, N);
+  const GemvSplit g = gemv_uses_mfma(a) ? gemv_split_mfma(a->m, a->k, N) : gemv_split(a->m, a->k, N);
   if (g.splits > 65535) return fail(LSFA_ERR_UNSUPPORTED, "k too large for one launch");
   if (g.bytes > 0) {
     if (!a->workspace) return fail(LSFA_ERR_INVALID, "workspace must be non-NULL");
@@ -565,7 +595,8 @@ int lsfa_gemv_group_check(const lsfa_gemv_group_args* a) {
 
 int lsfa_gemv_group_workspace_size(const lsfa_gemv_group_args* a, uint64_t* bytes) {
   if (a == nullptr || bytes == nullptr) return fail(LSFA_ERR_INVALID, "args or bytes is NULL");
-  *bytes = gemv_split(a->m, a->k, gemv_total_n(a)).bytes;
+  const long long N = gemv_total_n(a);
+  *bytes = (gemv_uses_mfma(a) ? gemv_split_mfma(a->m, a->k, N) : gemv_split(a->m, a->k, N)).bytes;
   return ok();
 }
 
@@ -574,7 +605,8 @@ int lsfa_gemv_group(const lsfa_gemv_group_args* a, void* stream) {
   if (rc) return rc;
   const long long N = gemv_total_n(a);
   if (a->m == 0 || N == 0) return ok();
-  const GemvSplit g = gemv_split(a->m, a->k, N);
+  const bool mfma = gemv_uses_mfma(a);
+  const GemvSplit g = mfma ? gemv_split_mfma(a->m, a->k, N) : gemv_split(a->m, a->k, N);
   lsfa::GemvParams p;
   memset(&p, 0, sizeof(p));
   p.x = a->x;
@@ -604,7 +636,8 @@ int lsfa_gemv_group(const lsfa_gemv_group_args* a, void* stream) {
   p.sx = a->x_stride;
   p.M = a->m; p.K = a->k; p.N = (int)N;
   p.kc = g.kc; p.splits = g.splits;
-  hipError_t e = lsfa::gemv(p, a->dtype == LSFA_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream));
+  hipError_t e = mfma ? lsfa::gemv_mfma(p, a->dtype == LSFA_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream))
+                      : lsfa::gemv(p, a->dtype == LSFA_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "gemv launch failed: %s", hipGetErrorString(e));
   return ok();
 }

@@ -13,10 +13,13 @@ single pass over B's bytes, so bf16/fp16 products with M <= 2 go to the
 library's skinny kernel (lsfa_gemv: one launch, a K-split pass over B at HBM
 rate whose last workgroup per column block sums the fp32 partials and rounds
 once), which hipBLASLt's general tiles reach at a fraction of the bandwidth.
-The kernel takes up to 8 rows (skinny_matmul), but its fp32 FMAs grow with
-the row count and, measured on MI355X over the LLaMA-3-8B decode projections,
-hipBLASLt overtakes it on some shapes from 3 rows on, so the automatic
-routing stops at 2.
+From 3 to 32 rows, plain products whose widths are multiples of 128 run on
+a second kernel that computes them on MFMA (W tiles through LDS, transposed
+reads); measured on MI355X over the LLaMA-3-8B decode projections it beats
+hipBLASLt up to 8 rows on the narrow products (q/k/v, o, down) but not on the
+wide ones (gate/up, LM head), so matmul routes 3-8 rows to it only for
+products of at most 8192 columns. The fused norm and SwiGLU inputs run on
+the first kernel and stay at up to 2 rows.
 
 Projections that share their input (a decoder's q/k/v, gate/up) go through
 matmul_shared_input, which runs them as one lsfa_gemv_group launch over their
@@ -39,8 +42,14 @@ import torch
 
 from .. import _lib
 
-SKINNY_MAX_ROWS = 8  # what lsfa_gemv takes
-AUTO_MAX_ROWS = 2    # what matmul, matmul_shared_input and swiglu_matmul route to it
+SKINNY_MAX_ROWS = 32  # what lsfa_gemv takes (more than 8 rows: MFMA kernel only)
+AUTO_MAX_ROWS = 2    # rows that every product (and the fused norm / SwiGLU inputs) routes to it
+# From 3 to 8 rows, plain products whose matrices are multiples of 128 columns
+# wide and total at most this many columns run on the library's MFMA kernel
+# (faster than hipBLASLt there: the q/k/v, o and down projections of a
+# decoder); wider ones (gate/up, the LM head) stay on hipBLASLt.
+MFMA_AUTO_ROWS = 8
+MFMA_AUTO_MAX_COLS = 8192
 
 _workspaces = {}  # (device index, stream handle) -> every workspace created for it, the last in use
 
@@ -55,9 +64,12 @@ def _workspace(device, stream, nbytes):
 
 
 def _skinny_ok(a: torch.Tensor, b: torch.Tensor, max_rows: int = SKINNY_MAX_ROWS) -> bool:
-    return (a.shape[0] <= max_rows and a.dtype in (torch.bfloat16, torch.float16)
-            and a.stride(1) == 1 and b.stride(1) == 1 and b.shape[1] % 8 == 0
-            and b.stride(0) % 8 == 0 and b.stride(0) >= b.shape[1] and b.data_ptr() % 16 == 0)
+    ok = (a.shape[0] <= max_rows and a.dtype in (torch.bfloat16, torch.float16)
+          and a.stride(1) == 1 and b.stride(1) == 1 and b.shape[1] % 8 == 0
+          and b.stride(0) % 8 == 0 and b.stride(0) >= b.shape[1] and b.data_ptr() % 16 == 0)
+    if ok and a.shape[0] > 8:  # the MFMA kernel's conditions
+        ok = (b.shape[1] % 128 == 0 and a.shape[1] % 8 == 0 and a.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0)
+    return ok
 
 
 def skinny_matmul(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
@@ -127,12 +139,23 @@ def skinny_matmul_group(a: torch.Tensor, bs, outs=None, gate: torch.Tensor = Non
     return outs
 
 
+def _auto_skinny(a: torch.Tensor, bs) -> bool:
+    """Whether matmul / matmul_shared_input route these products to the
+    skinny kernels (see AUTO_MAX_ROWS and MFMA_AUTO_*)."""
+    if not (len(bs) <= _lib.GEMV_MAX_GROUP and a.ndim == 2 and a.is_cuda and all(
+            b.ndim == 2 and b.is_cuda and b.dtype == a.dtype and b.shape[0] == a.shape[1] for b in bs)):
+        return False
+    if a.shape[0] <= AUTO_MAX_ROWS:
+        return all(_skinny_ok(a, b, AUTO_MAX_ROWS) for b in bs)
+    return (a.shape[0] <= MFMA_AUTO_ROWS and sum(b.shape[1] for b in bs) <= MFMA_AUTO_MAX_COLS
+            and all(_skinny_ok(a, b) and b.shape[1] % 128 == 0 for b in bs)
+            and a.shape[1] % 8 == 0 and a.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0)
+
+
 def matmul_shared_input(a: torch.Tensor, bs):
-    """[matmul(a, b) for b in bs]: one grouped skinny launch when every
-    product qualifies for the skinny kernel, else one matmul each."""
-    if len(bs) <= _lib.GEMV_MAX_GROUP and a.ndim == 2 and a.is_cuda and all(
-            b.ndim == 2 and b.is_cuda and b.dtype == a.dtype and b.shape[0] == a.shape[1]
-            and _skinny_ok(a, b, AUTO_MAX_ROWS) for b in bs):
+    """[matmul(a, b) for b in bs]: one grouped skinny launch when the
+    products qualify for the skinny kernels, else one matmul each."""
+    if _auto_skinny(a, bs):
         return skinny_matmul_group(a, bs)
     return [matmul(a, b) for b in bs]
 
@@ -200,6 +223,6 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     assert a.shape[1] == b.shape[0], f"inner dims must match: a is {tuple(a.shape)}, b is {tuple(b.shape)}"
     assert a.is_cuda and b.is_cuda, "the gfx950 path needs GPU tensors"
     assert a.dtype == b.dtype, f"dtype mismatch: a={a.dtype} b={b.dtype}"
-    if _skinny_ok(a, b, AUTO_MAX_ROWS):
+    if _auto_skinny(a, [b]):
         return skinny_matmul(a, b)
     return torch.matmul(a, b)

@@ -395,8 +395,14 @@ def test_abi_gemv_validation(built_library):
     assert _lib.gemv_check(_gemv_args())[0] == 0
     for m in range(1, 9):
         assert _lib.gemv_check(_gemv_args(m=m))[0] == 0
-    rc, msg = _lib.gemv_check(_gemv_args(m=9))
+    for m in (9, 16, 32):  # the MFMA kernel: widths multiples of 128, plain x
+        assert _lib.gemv_check(_gemv_args(m=m))[0] == 0
+    rc, msg = _lib.gemv_check(_gemv_args(m=33))
     assert rc == -2 and "8 rows" in msg
+    rc, msg = _lib.gemv_check(_gemv_args(m=9, n=4104, w_stride=4104))  # not a multiple of 128
+    assert rc == -2 and "8 rows" in msg
+    # MFMA workspace: K-ranges of 256 rows -> 16 splits at K = 4096
+    assert _lib.gemv_workspace_size(_gemv_args(m=16)) == 262144 + 16 * 16 * 4096 * 4
     rc, msg = _lib.gemv_check(_gemv_args(n=4092, w_stride=4096))
     assert rc == -2 and "n % 8" in msg
     rc, msg = _lib.gemv_check(_gemv_args(w=8194))
@@ -426,7 +432,7 @@ def test_abi_gemv_validation(built_library):
     assert rc == -2 and "columns" in msg
     _lib.gemv(_gemv_args(m=0, x=None, y=None), 0)  # empty: no-op, no GPU touched
     with pytest.raises(RuntimeError, match="8 rows"):
-        _lib.gemv(_gemv_args(m=9), 0)
+        _lib.gemv(_gemv_args(m=33), 0)
 
 
 def _group_args(ns, **kw):
