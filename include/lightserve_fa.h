@@ -319,7 +319,8 @@ typedef struct {
 
 /* Skinny GEMM for decode-time projections: y[M, N] = x[M, K] @ w[K, N] with
  * M <= 8 (up to 32 when every width is a multiple of 128, x rows are 16-byte
- * aligned and the input is plain x: those run on MFMA), w in the reference
+ * aligned and the input is x or x with a gate, not a norm: those run on
+ * MFMA), w in the reference
  * model's [in, out] row-major weight layout
  * (model/minimal_llama.py: every Linear is x @ w), bf16 or fp16, fp32
  * accumulate, one rounding. The reference calls its tiled GEMM for these

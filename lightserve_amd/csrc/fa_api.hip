@@ -469,9 +469,9 @@ struct GemvSplit {
 // width is a multiple of 128 and the input is plain x: K-ranges of at most 256
 // rows (four 64-row tiles per workgroup), 128-column blocks.
 bool gemv_uses_mfma(const lsfa_gemv_group_args* a) {
-  if (a->m < 3 || a->m > 32 || a->x_gate || a->norm_weight || a->k % 8 != 0 || a->x_stride % 8 != 0 ||
-      !aligned16(a->x))
+  if (a->m < 3 || a->m > 32 || a->norm_weight || a->k % 8 != 0 || a->x_stride % 8 != 0 || !aligned16(a->x))
     return false;
+  if (a->x_gate && (a->x_gate_stride % 8 != 0 || !aligned16(a->x_gate))) return false;
   long long n = 0;
   for (int i = 0; i < a->count; ++i) {
     if (a->n[i] % 128 != 0) return false;

@@ -63,15 +63,34 @@ __global__ __launch_bounds__(256) void fa_gemv_mfma_kernel(const GemvParams p) {
   // takes the same order: lane holds x[l32][16 step + 4hh .. + 3] and
   // x[l32][16 step + 8 + 4hh .. + 3]. Rows past M and columns past the range
   // are zero (the loads are clamped in bounds, then masked).
+  // With a gate the operand is bf16(bf16(silu(gate)) * x), the two roundings
+  // of F.silu(gate) * up.
   X8 xop[kMfmaTiles * 4];
   {
     const int m = min(l32, p.M - 1);
     const T* xr = (const T*)p.x + (int64_t)m * p.sx + k_begin;
+    const T* gr = p.xg != nullptr ? (const T*)p.xg + (int64_t)m * p.sxg + k_begin : nullptr;
+    auto load4 = [&](int k) -> u32x2 {
+      u32x2 v = *(const u32x2*)(xr + k);
+      if (gr != nullptr) {
+        const X4 up = __builtin_bit_cast(X4, v);
+        const X4 gt = __builtin_bit_cast(X4, *(const u32x2*)(gr + k));
+        X4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float gv = (float)gt[e];
+          const float act = (float)(T)(gv / (1.0f + expf(-gv)));
+          o[e] = (T)(act * (float)up[e]);
+        }
+        v = __builtin_bit_cast(u32x2, o);
+      }
+      return v;
+    };
 #pragma unroll
     for (int st = 0; st < kMfmaTiles * 4; ++st) {
       const int k0 = 16 * st + 4 * hh, k1 = k0 + 8;
-      u32x2 lo = *(const u32x2*)(xr + min(k0, k_len - 4));
-      u32x2 hi = *(const u32x2*)(xr + min(k1, k_len - 4));
+      u32x2 lo = load4(min(k0, k_len - 4));
+      u32x2 hi = load4(min(k1, k_len - 4));
       if (l32 >= p.M || k0 >= k_len) lo = u32x2{0u, 0u};
       if (l32 >= p.M || k1 >= k_len) hi = u32x2{0u, 0u};
       const u32x4 raw = {lo[0], lo[1], hi[0], hi[1]};

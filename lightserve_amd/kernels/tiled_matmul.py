@@ -18,8 +18,12 @@ a second kernel that computes them on MFMA (W tiles through LDS, transposed
 reads); measured on MI355X over the LLaMA-3-8B decode projections it beats
 hipBLASLt up to 8 rows on the narrow products (q/k/v, o, down) but not on the
 wide ones (gate/up, LM head), so matmul routes 3-8 rows to it only for
-products of at most 8192 columns. The fused norm and SwiGLU inputs run on
-the first kernel and stay at up to 2 rows.
+products of at most 8192 columns. The fused norm and SwiGLU inputs are
+routed at up to 2 rows only: the MFMA kernel takes a gate too, but every
+workgroup then evaluates the activation over its whole K-range for all 32
+padded rows before its first product, which measured slower (batch-8 decode
+step 1.043 ms) than torch's SiLU and multiply ahead of the plain product
+(0.885 ms).
 
 Projections that share their input (a decoder's q/k/v, gate/up) go through
 matmul_shared_input, which runs them as one lsfa_gemv_group launch over their
