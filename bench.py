@@ -16,8 +16,9 @@ Timing: W untimed warm-up steps; then K steps bracketed by
 torch.cuda.synchronize() on both sides; HIP events on the launch stream
 around each phase give the per-phase (per-launch) kernel time used for the
 forward TFLOP/s and the roofline. Correctness is re-checked against the
-oracle on two (batch, head) slices before timing, as the reference does
-(kernels/benchmark_flash_attention.py:104-106).
+oracle on every (batch, head) slice before timing, as the reference does
+(kernels/benchmark_flash_attention.py:104-106): o and lse, and dq/dk/dv when
+the step has a backward, all gated.
 
 The CPU baseline is the reference's test oracle (F.scaled_dot_product_attention
 in fp32 with autograd, kernels/tests/test_flash_attention_backward.py:86)
@@ -53,6 +54,9 @@ def parse_args():
                          "rope: in-place RoPE of config 3's q and k projections; "
                          "rmsnorm: fused residual add + RMSNorm, [2048, 8192] bf16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-parity", action="store_true",
+                    help="skip the oracle re-check before timing (profiler runs only, whose per-kernel counters "
+                         "should cover the timed kernels; the JSON line then says parity was not checked)")
     ap.add_argument("--no-sweep", action="store_true",
                     help="rmsnorm: skip the sweep over the reference's other shapes (profiler runs, whose "
                          "per-kernel averages must cover the headline shape only)")
@@ -77,27 +81,51 @@ def measured_traffic(kernel, workload):
 
 
 def check_parity(cfg, inp, outs):
-    """Oracle check of two (batch, head) slices (fp32 oracle on the GPU)."""
+    """Oracle check of every (batch, head) slice (fp32 oracle on the GPU).
+
+    o and lse against the closed form; dq/dk/dv against fp32 autograd. The
+    gate is max-abs <= 2e-2 and mean-abs <= 2e-3 (lse max-abs <= 1e-3); a
+    gradient that misses it passes only if it is within 1.5x of the error of
+    the reference's own algorithm (the restated tiled backward with its bf16
+    rounding points of P and dS), the rule the parity tests apply."""
     import torch
-    from oracle.attention import attention_grads, attention_reference
+    from oracle.attention import attention_grads, attention_reference, flash_backward_tiled
     q, k, v, causal = inp["q"], inp["k"], inp["v"], inp["causal"]
-    worst = {}
     B, H = q.shape[:2]
-    for b, h in ((0, 0), (B - 1, H - 1)):
-        sl = (slice(b, b + 1), slice(h, h + 1))
-        o_ref, lse_ref = attention_reference(q[sl], k[sl], v[sl], causal, dtype=torch.float32)
-        pairs = [("o", outs["o"][sl], o_ref), ("lse", outs["lse"][sl], lse_ref)]
-        if "dq" in outs:
-            g = attention_grads(q[sl], k[sl], v[sl], inp["do"][sl], causal, dtype=torch.float32)
-            pairs += [("dq", outs["dq"][sl], g[0]), ("dk", outs["dk"][sl], g[1]), ("dv", outs["dv"][sl], g[2])]
-        for name, got, ref in pairs:
-            err = (got.double() - ref.double()).abs()
-            mx, mn = err.max().item(), err.mean().item()
-            prev = worst.get(name, (0.0, 0.0))
-            worst[name] = (max(prev[0], mx), max(prev[1], mn))
-    res = {n: {"max_abs": float(f"{m:.3e}"), "mean_abs": float(f"{a:.3e}")} for n, (m, a) in worst.items()}
-    ok = all(res[n]["max_abs"] <= 2e-2 and res[n]["mean_abs"] <= 2e-3 for n in ("o",) if n in res)
-    ok = ok and res["lse"]["max_abs"] <= 1e-3
+    stats = {}  # name -> [max, sum of per-slice means, slices]
+
+    def add(key, got, ref):
+        err = (got.double() - ref.double()).abs()
+        st = stats.setdefault(key, [0.0, 0.0, 0])
+        st[0] = max(st[0], err.max().item())
+        st[1] += err.mean().item()
+        st[2] += 1
+
+    for b in range(B):
+        for h in range(H):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            o_ref, lse_ref = attention_reference(q[sl], k[sl], v[sl], causal, dtype=torch.float32)
+            add("o", outs["o"][sl], o_ref)
+            add("lse", outs["lse"][sl], lse_ref)
+            if "dq" in outs:
+                exact = attention_grads(q[sl], k[sl], v[sl], inp["do"][sl], causal, dtype=torch.float32)
+                alg = flash_backward_tiled(q[sl], k[sl], v[sl], o_ref.to(q.dtype), lse_ref, inp["do"][sl], causal,
+                                           block_n=256, op_dtype=q.dtype)
+                for name, ex, ra in zip(("dq", "dk", "dv"), exact, alg):
+                    add(name, outs[name][sl], ex)
+                    add(name + "_ref_alg", ra.to(q.dtype), ex)
+    res = {n: {"max_abs": float(f"{m:.3e}"), "mean_abs": float(f"{t / c:.3e}")} for n, (m, t, c) in stats.items()}
+    ok = res["o"]["max_abs"] <= 2e-2 and res["o"]["mean_abs"] <= 2e-3 and res["lse"]["max_abs"] <= 1e-3
+    for name in ("dq", "dk", "dv"):
+        if name not in res:
+            continue
+        r, a = res[name], res.pop(name + "_ref_alg")
+        gate = r["max_abs"] <= 2e-2 and r["mean_abs"] <= 2e-3
+        rel = r["max_abs"] <= 1.5 * a["max_abs"] and r["mean_abs"] <= 1.5 * a["mean_abs"]
+        r["rule"] = "gate" if gate else ("1.5x reference algorithm" if rel else "failed")
+        r["reference_algorithm"] = a
+        ok = ok and (gate or rel)
+    res["slices_checked"] = B * H
     return ok, res
 
 
@@ -790,6 +818,8 @@ def main():
         err = (o[cq[0]:cq[1]].transpose(0, 1).double() - o_ref.double()).abs()
         parity = {"o": {"max_abs": float(f"{err.max().item():.3e}"), "mean_abs": float(f"{err.mean().item():.3e}")}}
         parity_ok = parity["o"]["max_abs"] <= 2e-2 and parity["o"]["mean_abs"] <= 2e-3
+    elif args.skip_parity:
+        parity_ok, parity = None, {"skipped": "--skip-parity (profiler run)"}
     else:
         parity_ok, parity = check_parity(cfg, inp, outs)
     del outs
@@ -828,11 +858,46 @@ def main():
     fwd_tflops = f_fwd / (fwd_avg * 1e-3) / 1e12
 
     wl_key = f"config{args.config}"
-    traffic = measured_traffic("fa_fwd_kernel", wl_key)
-    roofline = {"kernel": "fa_fwd_kernel", "bound": "mfma", "achieved": round(fwd_tflops, 2),
-                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(fwd_tflops / PEAK_BF16_TFLOPS, 4),
-                "traffic": traffic,
-                "flops_per_launch": f_fwd, "avg_launch_ms": round(fwd_avg, 5)}
+    # Per-kernel launch times on the launch stream (HIP events around
+    # back-to-back launches): the forward from the timed steps; the backward's
+    # two kernels one at a time through lsfa_bwd's phase flags (the dK/dV
+    # phase reuses the workspace the dQ phase just wrote).
+    kernels = [{"kernel": "fa_fwd_kernel", "flops_per_launch": f_fwd, "mfma_flops_per_launch": f_fwd,
+                "avg_launch_ms": fwd_avg}]
+    if bwd is not None:
+        from lightserve_amd.kernels.flash_attention_backward import _backward_args
+        from lightserve_amd import _lib as lib
+        o_t, lse_t = fwd()
+        ba, keep = _backward_args(inp["do"], q, k, v, o_t, lse_t, inp["causal"])
+        raw = stream.cuda_stream
+        unit = f_fwd / 2  # one B*H*N^2*D GEMM (halved when causal)
+        for flag, name, alg_units, mfma_units in ((lib.BWD_ONLY_DQ, "fa_bwd_dq_kernel", 1, 3),
+                                                  (lib.BWD_ONLY_DKDV, "fa_bwd_dkdv_kernel", 4, 4)):
+            ba.flags = flag
+            for _ in range(2):
+                lib.bwd(ba, raw)
+            k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            k0.record(stream)
+            for _ in range(args.steps):
+                lib.bwd(ba, raw)
+            k1.record(stream)
+            torch.cuda.synchronize()
+            kernels.append({"kernel": name, "flops_per_launch": alg_units * unit,
+                            "mfma_flops_per_launch": mfma_units * unit,
+                            "avg_launch_ms": k0.elapsed_time(k1) / args.steps})
+        del keep
+    for kd in kernels:
+        kd["achieved"] = round(kd["flops_per_launch"] / (kd["avg_launch_ms"] * 1e-3) / 1e12, 2)
+        kd["frac"] = round(kd["achieved"] / PEAK_BF16_TFLOPS, 4)
+        kd["mfma_frac"] = round(kd["mfma_flops_per_launch"] / (kd["avg_launch_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+        kd["traffic"] = measured_traffic(kd["kernel"], wl_key)
+        kd["avg_launch_ms"] = round(kd["avg_launch_ms"], 5)
+    dom = max(kernels, key=lambda kd: kd["avg_launch_ms"])
+    roofline = {"kernel": dom["kernel"], "bound": "mfma", "achieved": dom["achieved"], "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": dom["frac"], "traffic": dom["traffic"],
+                "flops_per_launch": dom["flops_per_launch"], "avg_launch_ms": dom["avg_launch_ms"],
+                "kernels": kernels}
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),

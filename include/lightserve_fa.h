@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define LSFA_ABI_VERSION 7
+#define LSFA_ABI_VERSION 8
 
 typedef enum {
   LSFA_DTYPE_FP32 = 0,
@@ -126,8 +126,18 @@ typedef struct {
   int32_t head_dim;
   int32_t causal;
   float sm_scale;
-  int32_t reserved;
+  int32_t flags;               /* 0 (both kernels) or one LSFA_BWD_ONLY_* phase */
 } lsfa_bwd_args;
+
+/* lsfa_bwd_args.flags, for timing the two kernels of a bf16/fp16 backward
+ * one at a time (a profiler or benchmark; 0 runs both, in order):
+ * LSFA_BWD_ONLY_DQ runs the query-stationary kernel alone (it writes dq and
+ * the workspace's per-row (L*log2(e), delta)); LSFA_BWD_ONLY_DKDV runs the
+ * key-stationary kernel alone and reads those workspace values, so it needs
+ * a workspace that an earlier full or ONLY_DQ call with the same arguments
+ * filled. The fp32 path takes only 0. */
+#define LSFA_BWD_ONLY_DQ 1
+#define LSFA_BWD_ONLY_DKDV 2
 
 /* Paged-KV decode arguments: one new query token per sequence against a KV
  * cache addressed through block tables. The reference has no such kernel;

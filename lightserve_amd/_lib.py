@@ -13,7 +13,8 @@ import torch
 
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 8
+BWD_ONLY_DQ, BWD_ONLY_DKDV = 1, 2  # lsfa_bwd_args.flags: run one backward kernel (timing)
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
 TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}
@@ -62,7 +63,7 @@ class BwdArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32),
         ("heads_kv", ctypes.c_int32), ("seqlen_q", ctypes.c_int32), ("seqlen_k", ctypes.c_int32),
         ("head_dim", ctypes.c_int32), ("causal", ctypes.c_int32), ("sm_scale", ctypes.c_float),
-        ("reserved", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
     ]
 
 

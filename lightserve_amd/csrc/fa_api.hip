@@ -13,7 +13,7 @@
 namespace lsfa {
 hipError_t fwd_mfma(FwdParams p, bool is_bf16, int dp, bool causal, bool varlen, hipStream_t s);
 hipError_t fwd_paged(FwdParams p, bool is_bf16, int dp, bool causal, hipStream_t s);
-hipError_t bwd_mfma(const BwdParams& p, bool is_bf16, int dp, bool causal, hipStream_t s);
+hipError_t bwd_mfma(const BwdParams& p, bool is_bf16, int dp, bool causal, int phases, hipStream_t s);
 hipError_t fwd_f32(const FwdParams& p, int dp, bool causal, bool varlen, float scale, hipStream_t s);
 hipError_t bwd_f32(const BwdParams& p, int dp, bool causal, hipStream_t s);
 hipError_t decode_gqa(const DecodeParams& p, bool is_bf16, int dp, hipStream_t s);
@@ -221,6 +221,10 @@ int lsfa_bwd_check(const lsfa_bwd_args* a) {
   if (a->cu_seqlens_q != nullptr || a->cu_seqlens_k != nullptr)
     return fail(LSFA_ERR_UNSUPPORTED, "varlen backward is not implemented");
   if (a->heads_kv != a->heads_q) return fail(LSFA_ERR_UNSUPPORTED, "GQA backward is not implemented (heads_kv != heads_q)");
+  if (a->flags != 0 && a->flags != LSFA_BWD_ONLY_DQ && a->flags != LSFA_BWD_ONLY_DKDV)
+    return fail(LSFA_ERR_INVALID, "unknown flags %d", a->flags);
+  if (a->flags != 0 && a->dtype == LSFA_DTYPE_FP32)
+    return fail(LSFA_ERR_UNSUPPORTED, "the fp32 backward runs both phases together (flags must be 0)");
   const bool empty = (long long)a->batch * a->heads_q * (a->seqlen_q + a->seqlen_k) == 0;
   if (!empty) {
     if (!a->q || !a->k || !a->v || !a->o || !a->dout || !a->lse || !a->dq || !a->dk || !a->dv)
@@ -286,7 +290,8 @@ int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
   if (a->dtype == LSFA_DTYPE_FP32)
     e = lsfa::bwd_f32(p, dp, a->causal != 0, s);
   else
-    e = lsfa::bwd_mfma(p, a->dtype == LSFA_DTYPE_BF16, dp, a->causal != 0, s);
+    e = lsfa::bwd_mfma(p, a->dtype == LSFA_DTYPE_BF16, dp, a->causal != 0,
+                       a->flags == LSFA_BWD_ONLY_DQ ? 1 : (a->flags == LSFA_BWD_ONLY_DKDV ? 2 : 3), s);
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(e));
   return ok();
 }
@@ -466,8 +471,9 @@ struct GemvSplit {
 };
 
 // The MFMA kernel (fa_gemv_mfma.hip) serves 3..32 rows when every matrix's
-// width is a multiple of 128 and the input is plain x: K-ranges of at most 256
-// rows (four 64-row tiles per workgroup), 128-column blocks.
+// width is a multiple of 128 and the input is x or x with a SwiGLU gate (not a
+// fused norm): K-ranges of at most 256 rows (four 64-row tiles per
+// workgroup), 128-column blocks.
 bool gemv_uses_mfma(const lsfa_gemv_group_args* a) {
   if (a->m < 3 || a->m > 32 || a->norm_weight || a->k % 8 != 0 || a->x_stride % 8 != 0 || !aligned16(a->x))
     return false;
@@ -534,7 +540,7 @@ int lsfa_gemv_group_check(const lsfa_gemv_group_args* a) {
     return fail(LSFA_ERR_INVALID, "count must be 1..%d (count=%d)", LSFA_GEMV_MAX_GROUP, a->count);
   if (a->m < 0 || a->k < 0) return fail(LSFA_ERR_INVALID, "negative size (m=%d k=%d)", a->m, a->k);
   if (a->m > 8 && !gemv_uses_mfma(a))
-    return fail(LSFA_ERR_UNSUPPORTED, "gemv takes at most 8 rows, or 32 with plain x, widths that are multiples of "
+    return fail(LSFA_ERR_UNSUPPORTED, "gemv takes at most 8 rows, or 32 without a fused norm, widths that are multiples of "
                 "128 and 16-byte aligned x rows (m=%d)", a->m);
   for (int i = 0; i < a->count; ++i) {
     if (a->n[i] < 0) return fail(LSFA_ERR_INVALID, "negative size (n=%d)", a->n[i]);

@@ -527,19 +527,20 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   }
 }
 
+// phases: bit 0 the dq kernel, bit 1 the dk/dv kernel.
 template <typename T, int DP, bool CAUSAL>
-static hipError_t launch_bwd(BwdParams p, hipStream_t s) {
+static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
   // An empty axis means an empty grid: that kernel has nothing to write
   // (with no queries dK = dV = 0 still needs the dK/dV kernel, which then
   // runs no query tile).
   hipError_t e = hipSuccess;
   p.num_tiles = (p.Nq + 127) / 128;
-  if (p.num_tiles > 0) {
+  if ((phases & 1) && p.num_tiles > 0) {
     hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(256), 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   p.num_tiles = (p.Nk + 127) / 128;
-  if (p.num_tiles > 0) {
+  if ((phases & 2) && p.num_tiles > 0) {
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(512), 0, s, p);
     e = hipGetLastError();
   }
@@ -547,17 +548,17 @@ static hipError_t launch_bwd(BwdParams p, hipStream_t s) {
 }
 
 template <typename T>
-static hipError_t dispatch_bwd_t(const BwdParams& p, int dp, bool causal, hipStream_t s) {
+static hipError_t dispatch_bwd_t(const BwdParams& p, int dp, bool causal, int ph, hipStream_t s) {
   switch (dp) {
-    case 32: return causal ? launch_bwd<T, 32, true>(p, s) : launch_bwd<T, 32, false>(p, s);
-    case 64: return causal ? launch_bwd<T, 64, true>(p, s) : launch_bwd<T, 64, false>(p, s);
-    default: return causal ? launch_bwd<T, 128, true>(p, s) : launch_bwd<T, 128, false>(p, s);
+    case 32: return causal ? launch_bwd<T, 32, true>(p, ph, s) : launch_bwd<T, 32, false>(p, ph, s);
+    case 64: return causal ? launch_bwd<T, 64, true>(p, ph, s) : launch_bwd<T, 64, false>(p, ph, s);
+    default: return causal ? launch_bwd<T, 128, true>(p, ph, s) : launch_bwd<T, 128, false>(p, ph, s);
   }
 }
 
-hipError_t bwd_mfma(const BwdParams& p, bool is_bf16, int dp, bool causal, hipStream_t s) {
-  if (is_bf16) return dispatch_bwd_t<__bf16>(p, dp, causal, s);
-  return dispatch_bwd_t<_Float16>(p, dp, causal, s);
+hipError_t bwd_mfma(const BwdParams& p, bool is_bf16, int dp, bool causal, int phases, hipStream_t s) {
+  if (is_bf16) return dispatch_bwd_t<__bf16>(p, dp, causal, phases, s);
+  return dispatch_bwd_t<_Float16>(p, dp, causal, phases, s);
 }
 
 }  // namespace lsfa

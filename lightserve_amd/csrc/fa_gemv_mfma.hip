@@ -89,8 +89,13 @@ __global__ __launch_bounds__(256) void fa_gemv_mfma_kernel(const GemvParams p) {
 #pragma unroll
     for (int st = 0; st < kMfmaTiles * 4; ++st) {
       const int k0 = 16 * st + 4 * hh, k1 = k0 + 8;
-      u32x2 lo = load4(min(k0, k_len - 4));
-      u32x2 hi = load4(min(k1, k_len - 4));
+      // An empty K-range (k = 0, or a split past the end) loads nothing: the
+      // clamped index would fall before the row (uniform branch).
+      u32x2 lo = u32x2{0u, 0u}, hi = u32x2{0u, 0u};
+      if (k_len > 0) {
+        lo = load4(min(k0, k_len - 4));
+        hi = load4(min(k1, k_len - 4));
+      }
       if (l32 >= p.M || k0 >= k_len) lo = u32x2{0u, 0u};
       if (l32 >= p.M || k1 >= k_len) hi = u32x2{0u, 0u};
       const u32x4 raw = {lo[0], lo[1], hi[0], hi[1]};

@@ -29,14 +29,17 @@ def _flash_attention_forward_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
     return forward_into(q, k, v, causal, scale, True)
 
 
-def _flash_attention_backward(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                              o: torch.Tensor, L: torch.Tensor, causal: bool, sm_scale=None):
-    """Returns (dq, dk, dv) in the input dtype (dq like q, dk like k, dv like v)."""
+def _backward_args(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                   L: torch.Tensor, causal: bool, sm_scale=None):
+    """The lsfa_bwd arguments for these tensors, and what they point into:
+    (args, keep) with keep = (dq, dk, dv, the kernel-layout outputs, the
+    inputs' kernel-layout views or copies, workspace). None for an empty
+    problem."""
     B, H, N, D = q.shape
     scale = default_scale(D, sm_scale)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     if q.numel() == 0:
-        return dq, dk, dv
+        return None, (dq, dk, dv)
     dp = padded_head_dim(q)
     qk, kk, vk, ok_, dok = (as_kernel_layout(t, dp) for t in (q, k, v, o, do))
     outs = []
@@ -55,15 +58,26 @@ def _flash_attention_backward(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor
         dk_stride=_lib.strides4(dkk), dv_stride=_lib.strides4(dvk), lse_stride=_lib._i64x3(*L.stride()),
         cu_seqlens_q=None, cu_seqlens_k=None,
         dtype=_lib.TORCH_TO_LSFA[q.dtype], batch=B, heads_q=H, heads_kv=H, seqlen_q=N, seqlen_k=N,
-        head_dim=dp, causal=int(bool(causal)), sm_scale=scale, reserved=0,
+        head_dim=dp, causal=int(bool(causal)), sm_scale=scale, flags=0,
     )
     nbytes = _lib.bwd_workspace_size(args)
     # The caching allocator hands out 512-byte aligned blocks (the ABI asks for 256).
     workspace = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
     args.workspace, args.workspace_bytes = workspace.data_ptr(), nbytes
+    return args, (dq, dk, dv, (dqk, dkk, dvk), (qk, kk, vk, ok_, dok, L), workspace)
+
+
+def _flash_attention_backward(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              o: torch.Tensor, L: torch.Tensor, causal: bool, sm_scale=None):
+    """Returns (dq, dk, dv) in the input dtype (dq like q, dk like k, dv like v)."""
+    args, keep = _backward_args(do, q, k, v, o, L, causal, sm_scale)
+    dq, dk, dv = keep[:3]
+    if args is None:
+        return dq, dk, dv
     with torch.cuda.device(q.device):
         _lib.bwd(args, _lib.current_stream(q.device))
-    for t, tk in ((dq, dqk), (dk, dkk), (dv, dvk)):
+    D = q.shape[-1]
+    for t, tk in zip((dq, dk, dv), keep[3]):
         if tk is not t:
             t.copy_(tk[..., :D])
     return dq, dk, dv

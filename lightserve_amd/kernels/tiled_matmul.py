@@ -77,9 +77,10 @@ def _skinny_ok(a: torch.Tensor, b: torch.Tensor, max_rows: int = SKINNY_MAX_ROWS
 
 
 def skinny_matmul(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
-    """C = A @ B for a [M <= 8, K], b [K, N] (bf16/fp16, N % 8 == 0, rows of
+    """C = A @ B for a [M <= 32, K], b [K, N] (bf16/fp16, N % 8 == 0, rows of
     b 16-byte aligned) through lsfa_gemv; fp32 accumulation, one rounding."""
-    assert _skinny_ok(a, b), "skinny_matmul needs M <= 8, bf16/fp16, unit column strides, N % 8 == 0"
+    assert _skinny_ok(a, b), ("skinny_matmul needs M <= 8 (or up to 32 with N % 128 == 0 and 16-byte aligned a "
+                              "rows), bf16/fp16, unit column strides, N % 8 == 0")
     assert a.shape[1] == b.shape[0] and a.dtype == b.dtype and a.is_cuda and b.is_cuda, (
         "a [M, K] and b [K, N] must share K, dtype and device")
     M, K = a.shape

@@ -183,7 +183,7 @@ def test_abi_backward_validation(built_library):
                         dk_stride=st, dv_stride=st, lse_stride=_lib._i64x3(32, 8, 1),
                         cu_seqlens_q=None, cu_seqlens_k=None, dtype=_lib.DTYPE_BF16, batch=1,
                         heads_q=4, heads_kv=4, seqlen_q=8, seqlen_k=8, head_dim=64, causal=1,
-                        sm_scale=0.125, reserved=0)
+                        sm_scale=0.125, flags=0)
     assert _lib.bwd_check(args)[0] == 0
     args.heads_kv = 2
     rc, msg = _lib.bwd_check(args)
@@ -198,6 +198,17 @@ def test_abi_backward_validation(built_library):
     rc, msg = _lib.bwd_check(args)
     assert rc == -2 and "varlen" in msg
     args.cu_seqlens_q = args.cu_seqlens_k = None
+    # flags: 0 or one phase (LSFA_BWD_ONLY_DQ / ONLY_DKDV); the fp32 path takes only 0
+    for f in (_lib.BWD_ONLY_DQ, _lib.BWD_ONLY_DKDV):
+        args.flags = f
+        assert _lib.bwd_check(args)[0] == 0
+    args.flags = 3
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -1 and "flags" in msg
+    args.flags, args.dtype = _lib.BWD_ONLY_DQ, _lib.DTYPE_FP32
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -2 and "fp32" in msg
+    args.flags, args.dtype = 0, _lib.DTYPE_BF16
 
 
 def test_abi_backward_workspace(built_library):
@@ -211,7 +222,7 @@ def test_abi_backward_workspace(built_library):
                         dk_stride=st, dv_stride=st, lse_stride=_lib._i64x3(32, 8, 1),
                         cu_seqlens_q=None, cu_seqlens_k=None, dtype=_lib.DTYPE_BF16, batch=1,
                         heads_q=4, heads_kv=4, seqlen_q=8, seqlen_k=8, head_dim=64, causal=1,
-                        sm_scale=0.125, reserved=0)
+                        sm_scale=0.125, flags=0)
     rows = 1 * 4 * 128
     expected = rows * 8
     assert _lib.bwd_workspace_size(args) == expected
@@ -395,7 +406,7 @@ def test_abi_gemv_validation(built_library):
     assert _lib.gemv_check(_gemv_args())[0] == 0
     for m in range(1, 9):
         assert _lib.gemv_check(_gemv_args(m=m))[0] == 0
-    for m in (9, 16, 32):  # the MFMA kernel: widths multiples of 128, plain x
+    for m in (9, 16, 32):  # the MFMA kernel: widths multiples of 128, no fused norm
         assert _lib.gemv_check(_gemv_args(m=m))[0] == 0
     rc, msg = _lib.gemv_check(_gemv_args(m=33))
     assert rc == -2 and "8 rows" in msg

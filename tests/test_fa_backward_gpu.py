@@ -88,14 +88,16 @@ def _grads_gpu_fp32(q, k, v, do, causal):
 
 @pytest.mark.parametrize("cfg", [3, 4])
 def test_config_backward_full_size(gpu, cfg):
-    """The max-abs / mean-abs gate on dQ/dK/dV at the full config size, checked on a few
-    (batch, head) slices with the oracle's fp32 autograd on the GPU."""
+    """The max-abs / mean-abs gate on dQ/dK/dV at the full config size, on every
+    (batch, head) slice, with the oracle's fp32 autograd on the GPU (a gradient
+    that misses the gate must be within 1.5x of the reference algorithm's own
+    error, tests/gates.py)."""
     print(f"case config {cfg} backward full size", flush=True)
     inp = make_config_inputs(cfg, device=gpu)
     q, k, v, do, causal = inp["q"], inp["k"], inp["v"], inp["do"], inp["causal"]
     o, L = _flash_attention_forward_lse(q, k, v, causal)
     dq, dk, dv = _flash_attention_backward(do, q, k, v, o, L, causal)
-    slices = [(0, 0), (q.shape[0] - 1, q.shape[1] - 1)] if cfg == 3 else [(0, 3), (0, 12)]
+    slices = [(b, h) for b in range(q.shape[0]) for h in range(q.shape[1])]
     for b, h in slices:
         sl = (slice(b, b + 1), slice(h, h + 1))
         exact = _grads_gpu_fp32(q[sl], k[sl], v[sl], do[sl], causal)
@@ -109,7 +111,7 @@ def test_config_backward_full_size(gpu, cfg):
             assert_grad_parity(got, ex, ra, f"config {cfg} (b={b},h={h}) {name}")
 
 
-def _abi_fwd_bwd(q, k, v, do, causal, scale):
+def _abi_fwd_bwd(q, k, v, do, causal, scale, phases=(0,)):
     """Forward with L, then backward, through the C ABI directly (the Python
     mirror keeps the reference's square-only contract)."""
     from lightserve_amd import _lib
@@ -133,11 +135,13 @@ def _abi_fwd_bwd(q, k, v, do, causal, scale):
                       dq_stride=_lib.strides4(dq), dk_stride=_lib.strides4(dk), dv_stride=_lib.strides4(dv),
                       lse_stride=_lib._i64x3(*L.stride()), cu_seqlens_q=None, cu_seqlens_k=None, dtype=dt,
                       batch=B, heads_q=H, heads_kv=H, seqlen_q=Nq, seqlen_k=Nk, head_dim=D,
-                      causal=int(causal), sm_scale=scale, reserved=0)
+                      causal=int(causal), sm_scale=scale, flags=0)
     n = _lib.bwd_workspace_size(ba)
     ws = torch.empty(max(n, 1), device=q.device, dtype=torch.uint8)
     ba.workspace, ba.workspace_bytes = ws.data_ptr(), n
-    _lib.bwd(ba, stream)
+    for f in phases:
+        ba.flags = f
+        _lib.bwd(ba, stream)
     return o, L, dq, dk, dv
 
 
@@ -168,3 +172,19 @@ def test_abi_backward_non_square(gpu, Nq, Nk, causal, dtype):
     for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), refs):
         torch.testing.assert_close(got.cpu().double(), ref.nan_to_num(), atol=tol, rtol=tol,
                                    msg=lambda m: f"{name}: {m}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_abi_backward_phases(gpu, causal):
+    """lsfa_bwd with LSFA_BWD_ONLY_DQ, then LSFA_BWD_ONLY_DKDV on the same
+    workspace (the timing mode the benchmark uses) gives the full call's
+    gradients bit for bit."""
+    from lightserve_amd import _lib
+    print(f"case abi bwd phases causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(6)
+    q, k, v, do = (torch.randn(2, 3, 300, 128, generator=g).to(torch.bfloat16).to(gpu) for _ in range(4))
+    full = _abi_fwd_bwd(q, k, v, do, causal, 128 ** -0.5)
+    split = _abi_fwd_bwd(q, k, v, do, causal, 128 ** -0.5, phases=(_lib.BWD_ONLY_DQ, _lib.BWD_ONLY_DKDV))
+    torch.cuda.synchronize()
+    for a, b in zip(full, split):
+        assert torch.equal(a, b)

@@ -14,6 +14,7 @@ import torch
 
 from lightserve_amd.kernels.fused_rmsnorm_residual import fused_add_rmsnorm, rmsnorm
 from lightserve_amd.kernels.tiled_matmul import matmul
+from lightserve_amd import _lib
 from oracle.model import add_rmsnorm_reference
 
 pytestmark = pytest.mark.gpu
@@ -176,8 +177,9 @@ def test_skinny_matmul_counters_return_to_zero():
         torch.cuda.synchronize()
         assert torch.equal(first, again), (M, K, N)
         ws = tiled_matmul._workspaces[(0, torch.cuda.current_stream().cuda_stream)][-1]
-        blocks = (N + 255) // 256
-        assert (ws[:blocks * 64] == 0).all(), (M, K, N)
+        # the whole counter region: the VALU kernel keeps 16 counters per 256
+        # columns, the MFMA kernel (3 and 8 rows here) 16 per 128
+        assert (ws[:_lib.GEMV_COUNTER_BYTES] == 0).all(), (M, K, N)
 
 
 @pytest.mark.parametrize("M", [1, 3, 8])
@@ -290,3 +292,24 @@ def test_skinny_matmul_mfma_rows(M, dtype):
     ws = [(torch.randn(4096, n, device="cuda", generator=g) / 64).to(dtype) for n in (4096, 1024, 1024)]
     for c, w in zip(skinny_matmul_group(a, ws), ws):
         _assert_one_rounding(c, a, w)
+
+
+@pytest.mark.parametrize("M", [3, 8, 16, 32])
+def test_gemv_abi_empty_k(M):
+    """k = 0 through the C ABI at row counts the MFMA kernel takes (widths
+    multiples of 128): y must come back zero, and no x row may be read (x here
+    is a one-row, 16-byte allocation)."""
+    print(f"case gemv abi k=0 M={M}", flush=True)
+    N = 256
+    x = torch.zeros(8, device="cuda", dtype=torch.bfloat16)
+    w = torch.zeros(1, N, device="cuda", dtype=torch.bfloat16)
+    y = torch.full((M, N), float("nan"), device="cuda", dtype=torch.bfloat16)
+    args = _lib.GemvArgs(x=x.data_ptr(), w=w.data_ptr(), y=y.data_ptr(), workspace=None, workspace_bytes=0,
+                         x_stride=8, w_stride=N, y_stride=N, dtype=_lib.DTYPE_BF16, m=M, k=0, n=N)
+    assert _lib.gemv_check(args)[0] == 0
+    nbytes = _lib.gemv_workspace_size(args)
+    ws = torch.zeros(max(nbytes, 16), device="cuda", dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.gemv(args, _lib.current_stream(x.device))
+    torch.cuda.synchronize()
+    assert (y == 0).all()
