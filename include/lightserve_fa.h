@@ -453,6 +453,24 @@ int lsfa_bwd_workspace_size(const lsfa_bwd_args* args, uint64_t* bytes);
  * (:363-381) and the fp32->dtype cast of dq (:382). */
 int lsfa_bwd(const lsfa_bwd_args* args, void* stream);
 
+/* Allocation-free backward. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * training or serving loops that forbid allocation). Same arguments, kernels
+ * and results as lsfa_bwd, except that workspace and workspace_bytes are
+ * ignored: the workspace is a device array of LSFA_BWD_SCRATCH_BYTES inside
+ * the library (one per GPU, held while the library is loaded), so problems
+ * needing more (lsfa_bwd_workspace_size above that: batch * heads_q *
+ * seqlen_q rounded up to 128 above 2097152 rows) are rejected with
+ * LSFA_ERR_UNSUPPORTED. Calls share their GPU's array: two calls that can run
+ * at the same time on one GPU (different streams) race; calls in stream order
+ * do not. Nothing in the array needs clearing between calls (each call
+ * writes the per-row values before reading them; an LSFA_BWD_ONLY_DKDV call
+ * reads what the last full or ONLY_DQ call on that GPU left). The first call
+ * on a device looks up that device's copy of the array (a host query, not a
+ * stream operation). */
+#define LSFA_BWD_SCRATCH_BYTES 16777216
+int lsfa_bwd_noalloc(const lsfa_bwd_args* args, void* stream);
+
 /* Host-only validation of decode arguments; never touches the GPU. */
 int lsfa_decode_check(const lsfa_decode_args* args);
 

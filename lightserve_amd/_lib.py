@@ -14,6 +14,7 @@ import torch
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
 ABI_VERSION = 8
+BWD_SCRATCH_BYTES = 16777216  # LSFA_BWD_SCRATCH_BYTES: lsfa_bwd_noalloc's workspace limit
 BWD_ONLY_DQ, BWD_ONLY_DKDV = 1, 2  # lsfa_bwd_args.flags: run one backward kernel (timing)
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
@@ -22,7 +23,7 @@ TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfl
 STATUS = {0: "LSFA_OK", -1: "LSFA_ERR_INVALID", -2: "LSFA_ERR_UNSUPPORTED", -3: "LSFA_ERR_LAUNCH"}
 
 EXPORTED_SYMBOLS = ("lsfa_abi_version", "lsfa_last_error", "lsfa_fwd_check", "lsfa_fwd",
-                    "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd",
+                    "lsfa_bwd_check", "lsfa_bwd_workspace_size", "lsfa_bwd", "lsfa_bwd_noalloc",
                     "lsfa_decode_check", "lsfa_decode_workspace_size", "lsfa_decode",
                     "lsfa_rope_check", "lsfa_rope", "lsfa_rmsnorm_check", "lsfa_rmsnorm",
                     "lsfa_prefill_paged_check", "lsfa_prefill_paged",
@@ -200,7 +201,8 @@ def load():
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct)]
-        for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_decode", DecodeArgs),
+        for name, struct in (("lsfa_fwd", FwdArgs), ("lsfa_bwd", BwdArgs), ("lsfa_bwd_noalloc", BwdArgs),
+                             ("lsfa_decode", DecodeArgs),
                              ("lsfa_rope", RopeArgs), ("lsfa_rmsnorm", RmsNormArgs),
                              ("lsfa_prefill_paged", PrefillPagedArgs), ("lsfa_gemv", GemvArgs),
                              ("lsfa_gemv_group", GemvGroupArgs), ("lsfa_greedy", GreedyArgs)):
@@ -345,6 +347,12 @@ def fwd(args, stream):
 
 def bwd(args, stream):
     _raise_on(load().lsfa_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_bwd")
+
+
+def bwd_noalloc(args, stream):
+    """lsfa_bwd_noalloc: the backward with the library's own scratch array as
+    workspace (args.workspace is ignored)."""
+    _raise_on(load().lsfa_bwd_noalloc(ctypes.byref(args), ctypes.c_void_p(stream)), "lsfa_bwd_noalloc")
 
 
 def strides4(t):

@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/lightserve_fa.h"
@@ -258,9 +259,8 @@ int lsfa_bwd_workspace_size(const lsfa_bwd_args* a, uint64_t* bytes) {
   return ok();
 }
 
-int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
-  int rc = lsfa_bwd_check(a);
-  if (rc) return rc;
+// Launches the backward for validated arguments (the workspace included).
+static int run_bwd(const lsfa_bwd_args* a, void* stream) {
   if ((long long)a->batch * a->heads_q * (a->seqlen_q + a->seqlen_k) == 0) return ok();
   lsfa::BwdParams p;
   memset(&p, 0, sizeof(p));
@@ -294,6 +294,65 @@ int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
                        a->flags == LSFA_BWD_ONLY_DQ ? 1 : (a->flags == LSFA_BWD_ONLY_DKDV ? 2 : 3), s);
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
+  int rc = lsfa_bwd_check(a);
+  if (rc) return rc;
+  return run_bwd(a, stream);
+}
+
+// Allocation-free backward: the workspace is this file's device array
+// `scratch` (every GPU holds its own copy while the library is loaded). Host
+// code never uses the array's name as an address: each device's address comes
+// from hipGetSymbolAddress, resolved once per device on that device's first
+// call (with the device current) and kept in scratch_ptr.
+static __device__ __attribute__((aligned(256))) char scratch[LSFA_BWD_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(LSFA_ERR_UNSUPPORTED, "device index %d above %d", dev, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(LSFA_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return LSFA_OK;
+}
+}  // namespace
+
+int lsfa_bwd_noalloc(const lsfa_bwd_args* a, void* stream) {
+  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  uint64_t need = 0;
+  int rc = lsfa_bwd_workspace_size(a, &need);
+  if (rc) return rc;
+  if (need > (uint64_t)LSFA_BWD_SCRATCH_BYTES)
+    return fail(LSFA_ERR_UNSUPPORTED,
+                "lsfa_bwd_noalloc: this problem needs %llu bytes of workspace, above the %d bytes of the library's "
+                "scratch array (batch * heads * seqlen_q rounded up to 128 must be at most %d); use lsfa_bwd",
+                (unsigned long long)need, LSFA_BWD_SCRATCH_BYTES, LSFA_BWD_SCRATCH_BYTES / 8);
+  // Every argument is checked (host only) before any GPU query: the
+  // workspace fields first stand for the array (an aligned placeholder that
+  // the check never dereferences), then get its address on this device.
+  lsfa_bwd_args b = *a;
+  b.workspace = reinterpret_cast<void*>(uintptr_t{256});
+  b.workspace_bytes = LSFA_BWD_SCRATCH_BYTES;
+  if ((rc = lsfa_bwd_check(&b))) return rc;
+  b.workspace = nullptr;
+  if ((long long)a->batch * a->heads_q * (a->seqlen_q + a->seqlen_k) != 0 && need > 0)
+    if ((rc = scratch_for_current_device(&b.workspace))) return rc;
+  return run_bwd(&b, stream);
 }
 
 int lsfa_decode_check(const lsfa_decode_args* a) {

@@ -211,6 +211,27 @@ def test_abi_backward_validation(built_library):
     args.flags, args.dtype = 0, _lib.DTYPE_BF16
 
 
+def test_abi_backward_noalloc_limit(built_library):
+    """lsfa_bwd_noalloc rejects, before touching any GPU, a problem whose
+    workspace exceeds the library's scratch array (LSFA_BWD_SCRATCH_BYTES), and
+    validates its arguments as lsfa_bwd does."""
+    st = _lib._i64x4(2048, 512, 64, 1)
+    args = _lib.BwdArgs(q=16, k=32, v=48, o=64, dout=80, lse=96, dq=112, dk=128, dv=144, workspace=None,
+                        workspace_bytes=0,
+                        q_stride=st, k_stride=st, v_stride=st, o_stride=st, do_stride=st, dq_stride=st,
+                        dk_stride=st, dv_stride=st, lse_stride=_lib._i64x3(32, 8, 1),
+                        cu_seqlens_q=None, cu_seqlens_k=None, dtype=_lib.DTYPE_BF16, batch=4,
+                        heads_q=32, heads_kv=32, seqlen_q=16385, seqlen_k=16385, head_dim=64, causal=1,
+                        sm_scale=0.125, flags=0)
+    assert _lib.bwd_workspace_size(args) > _lib.BWD_SCRATCH_BYTES
+    rc = _lib.load().lsfa_bwd_noalloc(ctypes.byref(args), None)
+    assert rc == -2 and "scratch" in _lib.load().lsfa_last_error().decode()
+    args.heads_kv = 16  # GQA backward: rejected like lsfa_bwd
+    args.seqlen_q = args.seqlen_k = 128
+    rc = _lib.load().lsfa_bwd_noalloc(ctypes.byref(args), None)
+    assert rc == -2 and "GQA" in _lib.load().lsfa_last_error().decode()
+
+
 def test_abi_backward_workspace(built_library):
     """Workspace size: (L*log2e, delta) fp32 pairs for every (b, h, query) with
     queries padded to 128, 256-byte aligned. Too small or misaligned
