@@ -109,10 +109,21 @@ __device__ __forceinline__ float half_sum(float x) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // 16-byte segment swizzle of LDS tiles stored [rows][DP]. Rows r..r+15 read
-// at one segment (K operand, ds_read_b128) and 4x4 blocks of (row, segment)
-// (transpose reads) both land on distinct bank groups.
+// at one segment (K operand, ds_read_b128) and 4-row x 32-byte blocks
+// (transpose reads) both land on distinct banks (64 banks of 4 bytes, i.e.
+// 16 segment slots per 256 bytes). With 256-byte rows (DP = 128) every row
+// starts at slot 0, so the 16 rows need 16 distinct swizzles. With 128-byte
+// rows (DP = 64) rows alternate between slots 0..7 and 8..15, so rows of one
+// parity need 8 distinct swizzles, and rows 4q and 4q + 2 (and 4q + 1, 4q + 3)
+// must differ in bit 2 so that their 32-byte transpose-read spans do not
+// meet: swizzle = bit-rotated (row / 2) % 8. With 64-byte rows (DP = 32) four
+// rows share 256 bytes; rows r and r + 4 need distinct swizzles.
 template <int DP>
 __device__ __forceinline__ int seg_swz(int row) {
+  if constexpr (DP == 64) {
+    const int e = (row >> 1) & 7;
+    return ((e & 1) << 2) | (e >> 1);
+  }
   return (((row & 3) << 2) | ((row >> 2) & 3)) & (DP / 8 - 1);
 }
 // Element offset of (row, col) inside a swizzled [rows][DP] LDS tile; col%8
