@@ -33,6 +33,14 @@ CXXFLAGS = [
 ]
 
 
+# Per-source additions. fa_bwd.hip: MFMA results in VGPRs. The dK/dV kernel
+# runs one wave per SIMD, where the compiler would otherwise put every MFMA
+# accumulator in AGPRs and copy S and dP back to VGPRs for the softmax (one
+# v_accvgpr_read per element); with VGPR results only the long-lived dK/dV
+# sums spill to AGPRs.
+EXTRA_FLAGS = {"fa_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _hipcc():
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -42,7 +50,7 @@ def _hipcc():
 
 def _compile(src):
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [_hipcc(), *CXXFLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [_hipcc(), *CXXFLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(HERE, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)

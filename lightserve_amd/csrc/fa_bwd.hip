@@ -256,51 +256,46 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV. Workgroup = 8 waves (two per SIMD, at most 256 registers each)
-// over 128 keys; K and V of those keys stay in LDS for the whole kernel.
-// Every operand reaches LDS with buffer_load ... lds (no register staging):
-// per 64-query tile, the row-major Q/dO tile with L*log2e and delta, in two
-// stages. Wave w owns keys 32*(w%4)..+31 and query rows 32*(w/4)..+31 of
-// every tile:
-//   S  = Q K^T            A = Q rows (LDS),   B = K rows (LDS)
-//   dP = dO V^T           A = dO rows (LDS),  B = V rows (LDS)
-//   P  = exp2(S*scale*log2e - L*log2e), dS = P (dP - delta)
-//   dV^T += dO^T P        A = dO^T (transpose reads of the dO rows), B = P
-//   dK^T += Q^T dS        A = Q^T (transpose reads of the Q rows),   B = dS
-// The two waves of a SIMD (same keys, the two query halves) run half a tile
-// apart (see the loop), so one's softmax VALU work overlaps the other's
-// dV/dK MFMAs.
-// The two query halves' partial dK/dV are summed through LDS at the end.
-// Query rows beyond the sequence have L = +inf in the workspace (written by
-// the dq kernel's prologue), so their P is exactly 0; head-dim columns at or
-// past D load as zero.
+// dK, dV. Workgroup = 4 waves, one per SIMD, over 128 keys; wave w owns keys
+// 32w..32w+31 and keeps their K and V rows in registers for the whole kernel
+// (the B operands of S = Q K^T and dP = dO V^T). Q, dO and the rows'
+// (L*log2e, delta) pairs stream through three LDS stages of 64-row tiles by
+// direct buffer loads. Each wave walks the 32-row halves of the tiles in
+// order, software-pipelined so that its own MFMA and VALU work overlap (a
+// wave's MFMAs run beside its own independent VALU instructions, not beside
+// another wave's):
+//   iteration h:  S, dP of half h+1 (16 MFMAs, A = Q / dO rows from LDS)
+//                 beside P = exp2(S*scale*log2e - L*log2e), dS = P (dP - delta)
+//                 of half h (VALU), then
+//                 dV^T += dO^T P and dK^T += Q^T dS of half h (16 MFMAs, A =
+//                 dO^T / Q^T through transpose reads of the same row tiles).
+// A tile's stage is refilled after every wave has finished its second half
+// (one barrier per tile); a tile is loaded three halves-iterations before its
+// first use. Query rows beyond the sequence have L = +inf in the workspace
+// (written by the dq kernel's prologue), so their P is exactly 0; head-dim
+// columns at or past D load as zero. dK is scaled by sm_scale at the end.
 // ---------------------------------------------------------------------------
 template <typename T, int DP, bool CAUSAL>
-__global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
-  constexpr int NW = 8, BNK = 128, BMQ = 64;
+  constexpr int NW = 4, BNK = 128, BMQ = 64, NST = 3;
   constexpr int KSTEPS = DP / 16, DT = DP / 32;
-  constexpr int KV_B = BNK * DP * 2;  // bytes of K (or V)
-  constexpr int R_B = BMQ * DP * 2;   // bytes of a row-major Q (or dO) tile
-  // Two row stages, each Q | dO | (L*log2e, delta) pairs, 1 KB aligned.
-  constexpr int RS_B = 2 * R_B + 1024;
-  constexpr int OFF_K = 0, OFF_V = KV_B, OFF_R = 2 * KV_B;
-  constexpr int LDS_B = OFF_R + 2 * RS_B;
-  constexpr int NG = 2 * DT * 4;  // f32x4 groups of dK^T and dV^T per lane
-  static_assert((NW / 2) * NG * 64 * 16 <= LDS_B, "epilogue does not fit in LDS");
-  constexpr int CKV = 2 * KV_B / 1024 / NW;  // 1 KB chunks per wave: K|V
-  constexpr int CR = 2 * R_B / 1024 / NW;    //                        Q|dO rows
-  static_assert(CKV >= 1 && CR >= 1, "tile too small for the workgroup");
+  constexpr int R_B = BMQ * DP * 2;     // bytes of a row-major Q (or dO) tile
+  constexpr int RS_B = 2 * R_B + 1024;  // one stage: Q | dO | (L*log2e, delta) pairs, 1 KB aligned
+  constexpr int LDS_B = NST * RS_B;
+  constexpr int CR = 2 * R_B / 1024 / NW;  // 1 KB chunks per wave per tile (Q|dO)
+  static_assert(CR >= 1, "tile too small for the workgroup");
+  static_assert(LDS_B <= 160 * 1024, "LDS budget");
 
   __shared__ __attribute__((aligned(1024))) char sm_raw[LDS_B];
   LDS_AS char* sm = (LDS_AS char*)sm_raw;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
-  const int kb = wave & 3, qh = wave >> 2;
-  const bool w_hi = wave >= NW / 2;  // waves 4..7 load V and dO; 0..3 load K and Q
+  const int kb = wave;
+  const bool w_hi = wave >= NW / 2;  // waves 2, 3 load dO; 0, 1 load Q
   int bh, kt;
   map_tile(p.num_tiles, gridDim.x, bh, kt, false);  // low key tiles see the most queries
   const int b = bh / p.H, h = bh - b * p.H;
@@ -308,66 +303,66 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   const int k0 = kt * BNK;
   const int off = nk - nq;
 
-  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh + (int64_t)k0 * p.skn;
-  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh + (int64_t)k0 * p.svn;
+  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh;
+  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh;
   const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
   const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
   const float* LD = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh;
 
-  // Lane byte offset of row-major chunk lc (tile rows of 2*DP bytes): lane t
-  // fills stored segment (byte % 2DP)/16, which holds logical segment
-  // stored ^ seg_swz(row). Logical columns at or past D get an offset past
-  // any descriptor's end, so they read as zero.
+  const int n_qt = (nq + BMQ - 1) / BMQ;  // every tile starts below nq
+  int t_begin = 0;
+  if (CAUSAL) t_begin = max(0, k0 - off) / BMQ;  // first tile holding a query that sees key k0
+  const int n_t = max(0, n_qt - t_begin);
+  const int kcol = k0 + 32 * kb + l32;  // this lane's key
+
+  // Row-major tile loads (see fa_bwd_dq_kernel's row_voff).
   auto row_voff = [&](int lc, int64_t sn) -> int {
     const int byte = lc * 1024 + lane * 16;
     const int row = byte / (DP * 2);
     const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
     return seg * 8 < D ? (int)(row * sn * 2) + seg * 16 : (int)0x80000000;
   };
-
-  // K and V of the 128 keys (rows past nk read as zero).
-  {
-    const int rows = max(0, min(BNK, nk - k0));
-    const int64_t sn = w_hi ? p.svn : p.skn;
-    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(w_hi ? V : K, (int)(rows * sn * 2));
-#pragma unroll
-    for (int i = 0; i < CKV; ++i) {
-      const int c = wave * CKV + i;  // chunk of the K|V region
-      const int vo = row_voff(c % (KV_B / 1024), sn);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(sm + OFF_K + c * 1024), 16, vo, 0, 0, 0);
-    }
-  }
-
   int rvo[CR];
 #pragma unroll
   for (int i = 0; i < CR; ++i) rvo[i] = row_voff((wave % (NW / 2)) * CR + i, w_hi ? p.sdon : p.sqn);
-
-  // (Offset arrays go in as pointers and lambda results are hoisted into
-  // locals: an array-reference lambda parameter, or a lambda call inside a
-  // builtin's argument list, makes clang's host pass silently drop the
-  // kernel's launch stub.)
-  auto load_rows = [&](int t, int stage, const int* vo) {
+  auto load_tile = [&](int t, int stage, const int* vo) {
     const int q0 = t * BMQ;
     const int rows = min(nq - q0, BMQ);
     const int64_t sn = w_hi ? p.sdon : p.sqn;
     const __amdgpu_buffer_rsrc_t rs = tile_rsrc((w_hi ? dO : Q) + (int64_t)q0 * sn, (int)(rows * sn * 2));
-    LDS_AS char* base = sm + OFF_R + stage * RS_B;
+    LDS_AS char* base = sm + stage * RS_B + (w_hi ? R_B : 0);
 #pragma unroll
     for (int i = 0; i < CR; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(base + (wave * CR + i) * 1024), 16, vo[i], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(base + ((wave % (NW / 2)) * CR + i) * 1024), 16,
+                                               vo[i], 0, 0, 0);
     if (wave == 0 && lane < BMQ * 8 / 16) {
       const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(LD + 2 * (int64_t)q0, BMQ * 8);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (LDS_AS void*)(base + 2 * R_B), 16, lane * 16, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (LDS_AS void*)(sm + stage * RS_B + 2 * R_B), 16, lane * 16, 0, 0,
+                                               0);
     }
   };
+  // The first three tiles go in flight before the K / V register loads.
+#pragma unroll
+  for (int i = 0; i < NST; ++i)
+    if (i < n_t) load_tile(t_begin + i, i, rvo);
 
-  // LDS read offsets. Row-major tiles: the swizzle depends on row & 15, so
-  // the wave's 32-row blocks are plain byte offsets; Q^T and dO^T come from
-  // the same row-major tiles through transpose reads (16-query steps).
+  // K and V rows of this lane's key as B operands: columns 16kk + 8hh .. +7.
+  X8 kreg[KSTEPS], vreg[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    const int col = 16 * kk + 8 * hh;
+    u32x4 kr = {0, 0, 0, 0}, vr = {0, 0, 0, 0};
+    if (kcol < nk && col < D) {
+      kr = ldg16(K + (int64_t)kcol * p.skn + col);
+      vr = ldg16(V + (int64_t)kcol * p.svn + col);
+    }
+    kreg[kk] = __builtin_bit_cast(X8, kr);
+    vreg[kk] = __builtin_bit_cast(X8, vr);
+  }
+
   int roff[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) roff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
-  const int qrow_b = 32 * qh * DP * 2, krow_b = 32 * kb * DP * 2;
   const int tr_row = 4 * hh + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   int troff[DT][2];
@@ -384,125 +379,198 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     dv[dt] = f32x16{};
   }
   const float sl2 = p.scale_log2;
-  const int n_qt = (nq + BMQ - 1) / BMQ;  // every tile starts below nq
-  int t_begin = 0;
-  if (CAUSAL) t_begin = max(0, k0 - off) / BMQ;  // first tile holding a query that sees key k0
-  const int kcol = k0 + 32 * kb + l32;            // this lane's key
-  const int n_t = max(0, n_qt - t_begin);
 
-  // The two query halves run half a tile apart, so that on every SIMD one
-  // wave computes S, dP and the softmax (MFMA then VALU) while its partner
-  // (same keys, other query half) accumulates dV and dK (MFMA only). Step
-  // 2i of a wave is phase 1 of its i-th tile, step 2i+1 phase 2; the qh = 1
-  // waves are one step behind, so tile i's rows are read in segments 2i ..
-  // 2i+2 and tile i+2 (same row stage) loads during segment 2i+3.
-  X8 P0{}, P1{}, G0{}, G1{};  // phase 1 -> phase 2 of the same tile
-  auto phase1 = [&](int t, const LDS_AS char* st) {
-    const int q0 = t * BMQ;
-    f32x16 s = f32x16{}, dp = f32x16{};
-    __builtin_amdgcn_s_setprio(1);
+  // Half (t, q): rows 32 q .. 32 q + 31 of tile t_begin + t, which sits in
+  // LDS stage t % NST. The loop below is unrolled over the stages so that
+  // every LDS address is a lane offset plus an immediate. Within a wave the
+  // work of two halves is interleaved in fenced chunks (the scheduler keeps
+  // each chunk's instructions together and in order), so that the wave's
+  // MFMAs issue beside its own independent VALU and LDS instructions:
+  //   phase X: 16 chunks of (S or dP MFMA of the next half, operand read
+  //            PF chunks ahead; P and dS of one score of this half; at
+  //            chunks 8..15 one conversion of P0 / G0),
+  //   phase Y: 16 chunks of (two transpose reads PF chunks ahead; one dV or
+  //            dK MFMA of this half, the 16-query step ks = 0 first; at
+  //            chunks 0..7 one conversion of P1 / G1).
+  // Register i of a score tile holds query 32 q + 8 (i / 4) + 4 hh + i % 4.
+  constexpr int PF = 3;
+  typedef __attribute__((ext_vector_type(2))) T T2;
+  auto cvt2 = [](float a, float b) -> uint32_t { return __builtin_bit_cast(uint32_t, T2{(T)a, (T)b}); };
+  u32x4 p0w, g0w, p1w, g1w;  // P0, G0, P1, G1 as packed words
+  X8 P0, P1, G0, G1;
+
+  // Phase X has NCX = 2 KSTEPS MFMA chunks and EPC = 16 / NCX scores per
+  // chunk; phase Y has NCY = 4 DT chunks, the first 2 DT of them (step ks = 0)
+  // carrying the 8 conversions of P1 / G1 that the rest need.
+  constexpr int NCX = 2 * KSTEPS, EPC = 16 / NCX, NCY = 4 * DT, CPY = 8 / (2 * DT);
+  auto phase_x = [&](const LDS_AS char* nst, int nq, f32x16& sn, f32x16& dn, const LDS_AS char* stg, int t, int q,
+                     f32x16& s, f32x16& dp) {
+    const LDS_AS char* an = nst + 32 * nq * DP * 2;
+    // operand c: kk = c / 2; even c reads a Q row (S), odd c a dO row (dP)
+    auto opread = [&](int c) -> X8 { return *(const LDS_AS X8*)(an + (c & 1) * R_B + roff[c >> 1]); };
+    // (L*log2e, delta) of queries 8g + 4hh .. +3 (group g = scores 4g .. 4g+3,
+    // 8-byte pairs at byte 64 g): two 16-byte reads, issued four chunks
+    // before the group's first score is scaled.
+    const LDS_AS f32x4* ldp = (const LDS_AS f32x4*)(stg + 2 * R_B + (32 * q + 4 * hh) * 8);
+    f32x4 lda[4], ldc[4];
+    auto lead = [](int g) { return 4 * g / EPC - 4; };
+    auto l2_of = [&](int i) { const int g = i >> 2, e = i & 3; return e < 2 ? lda[g][2 * e] : ldc[g][2 * (e - 2)]; };
+    auto dl_of = [&](int i) { const int g = i >> 2, e = i & 3; return e < 2 ? lda[g][2 * e + 1] : ldc[g][2 * (e - 2) + 1]; };
+    // Each score goes through three steps two chunks apart (x = s*scale*log2e
+    // - L*log2e; p = exp2(x); dS = p (dP - delta)), so the VALU instructions
+    // of one chunk never wait on each other.
+    auto step_a = [&](int cc) {
+      if (cc < NCX)
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      s = mfma32(*(const LDS_AS X8*)(st + qrow_b + roff[kk]), *(const LDS_AS X8*)(sm + OFF_K + krow_b + roff[kk]), s);
-      dp = mfma32(*(const LDS_AS X8*)(st + R_B + qrow_b + roff[kk]),
-                  *(const LDS_AS X8*)(sm + OFF_V + krow_b + roff[kk]), dp);
-    }
-    __builtin_amdgcn_s_setprio(0);
-    // Register i holds query q0 + 32*qh + 8*(i/4) + 4*hh + i%4 of key kcol;
-    // (L*log2e, delta) of those four consecutive queries are two 16-byte reads.
+        for (int u = 0; u < EPC; ++u) { const int i = cc * EPC + u; s[i] = fmaf(s[i], sl2, -l2_of(i)); }
+    };
+    auto step_b = [&](int cc) {
+      if (cc < NCX)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const LDS_AS f32x4* ldp = (const LDS_AS f32x4*)(st + 2 * R_B + (32 * qh + 8 * j + 4 * hh) * 8);
-      const f32x4 a = ldp[0], c = ldp[1];
-      const float l2v[4] = {a[0], a[2], c[0], c[2]};
-      const float dlv[4] = {a[1], a[3], c[1], c[3]};
+        for (int u = 0; u < EPC; ++u) { const int i = cc * EPC + u; s[i] = fast_exp2(s[i]); }
+    };
+    auto step_c = [&](int cc) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 4 * j + e;
-        const float pv = fast_exp2(fmaf(s[i], sl2, -l2v[e]));
-        s[i] = pv;
-        dp[i] = pv * (dp[i] - dlv[e]);
+      for (int u = 0; u < EPC; ++u) { const int i = cc * EPC + u; dp[i] = s[i] * (dp[i] - dl_of(i)); }
+    };
+    X8 op[PF + 1];
+#pragma unroll
+    for (int c = 0; c < PF && c < NCX; ++c) op[c] = opread(c);
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      if (lead(g) < 0) {
+        lda[g] = ldp[4 * g];
+        ldc[g] = ldp[4 * g + 1];
       }
+    sn = f32x16{};
+    dn = f32x16{};
+    step_a(0);
+    step_a(1);
+    step_b(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < NCX; ++c) {
+      if (c + PF < NCX) op[(c + PF) % (PF + 1)] = opread(c + PF);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        if (lead(g) == c) {
+          lda[g] = ldp[4 * g];
+          ldc[g] = ldp[4 * g + 1];
+        }
+      if (c & 1)
+        dn = mfma32(op[c % (PF + 1)], vreg[c >> 1], dn);
+      else
+        sn = mfma32(op[c % (PF + 1)], kreg[c >> 1], sn);
+      step_a(c + 2);
+      step_b(c + 1);
+      step_c(c);
+      if (c >= NCX / 2) {  // scores 0..7 are final: P0 / G0 words
+#pragma unroll
+        for (int u = 0; u < EPC; ++u) {
+          const int k = (c - NCX / 2) * EPC + u, w = k >> 1;
+          if ((k & 1) == 0) p0w[w] = cvt2(s[2 * w], s[2 * w + 1]);
+          else g0w[w] = cvt2(dp[2 * w], dp[2 * w + 1]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (CAUSAL && k0 + 32 * kb + 31 > q0 + 32 * qh + off) {  // block crosses the diagonal
-      const int lim = kcol - (q0 + 32 * qh + 4 * hh + off);  // masked if 8*(i/4) + i%4 < lim
+    const int q0 = (t_begin + t) * BMQ + 32 * q;
+    if (CAUSAL && k0 + 32 * kb + 31 > q0 + off) {  // block crosses the diagonal
+      // (the empty volatile asm keeps this a branch: the selects below would
+      // otherwise be hoisted out of it and run on every half)
+      asm volatile("" ::: "memory");
+      const int lim = kcol - (q0 + 4 * hh + off);  // masked if 8*(i/4) + i%4 < lim
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const bool m = 8 * (i >> 2) + (i & 3) < lim;
         s[i] = m ? 0.f : s[i];
         dp[i] = m ? 0.f : dp[i];
       }
-    }
-    P0 = pack8<T>(s, 0);
-    P1 = pack8<T>(s, 8);
-    G0 = pack8<T>(dp, 0);
-    G1 = pack8<T>(dp, 8);
-  };
-  auto phase2 = [&](const LDS_AS char* st) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const LDS_AS char* qb = st + (32 * qh + 16 * ks) * DP * 2;
-        const X8 ado = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(qb + R_B + troff[dt][0])),
-                                    lds_read_tr((const LDS_AS T*)(qb + R_B + troff[dt][1])));
-        const X8 aq = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(qb + troff[dt][0])),
-                                   lds_read_tr((const LDS_AS T*)(qb + troff[dt][1])));
-        dv[dt] = mfma32(ado, ks == 0 ? P0 : P1, dv[dt]);
-        dk[dt] = mfma32(aq, ks == 0 ? G0 : G1, dk[dt]);
+      for (int w = 0; w < 4; ++w) {
+        p0w[w] = cvt2(s[2 * w], s[2 * w + 1]);
+        g0w[w] = cvt2(dp[2 * w], dp[2 * w + 1]);
       }
+    }
+    P0 = __builtin_bit_cast(X8, p0w);
+    G0 = __builtin_bit_cast(X8, g0w);
+  };
+  auto phase_y = [&](const LDS_AS char* stg, int q, const f32x16& s, const f32x16& dp) {
+    const LDS_AS char* st = stg + 32 * q * DP * 2;
+    // MFMA c: ks = c / (2 DT), dt = (c / 2) % DT; even c is dV (dO^T), odd c dK (Q^T)
+    auto opread = [&](int c) -> X8 {
+      const LDS_AS char* qb = st + 16 * (c / (2 * DT)) * DP * 2 + ((c & 1) ? 0 : R_B);
+      const int dt = (c >> 1) % DT;
+      return cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(qb + troff[dt][0])),
+                          lds_read_tr((const LDS_AS T*)(qb + troff[dt][1])));
+    };
+    X8 op[PF + 1];
+#pragma unroll
+    for (int c = 0; c < PF && c < NCY; ++c) op[c] = opread(c);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < NCY; ++c) {
+      if (c + PF < NCY) op[(c + PF) % (PF + 1)] = opread(c + PF);
+      if (c < 2 * DT) {  // scores 8..15: P1 / G1 words
+#pragma unroll
+        for (int u = 0; u < CPY; ++u) {
+          const int k = c * CPY + u, w = k >> 1;
+          if ((k & 1) == 0) p1w[w] = cvt2(s[8 + 2 * w], s[9 + 2 * w]);
+          else g1w[w] = cvt2(dp[8 + 2 * w], dp[9 + 2 * w]);
+        }
+        if (c == 2 * DT - 1) {
+          P1 = __builtin_bit_cast(X8, p1w);
+          G1 = __builtin_bit_cast(X8, g1w);
+        }
+      }
+      const int dt = (c >> 1) % DT, ks = c / (2 * DT);
+      if (c & 1)
+        dk[dt] = mfma32(op[c % (PF + 1)], ks == 0 ? G0 : G1, dk[dt]);
+      else
+        dv[dt] = mfma32(op[c % (PF + 1)], ks == 0 ? P0 : P1, dv[dt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // S and dP of the first half (not interleaved).
+  auto scores = [&](const LDS_AS char* stg, int q, f32x16& s, f32x16& dp) {
+    const LDS_AS char* st = stg + 32 * q * DP * 2;
+    s = f32x16{};
+    dp = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      s = mfma32(*(const LDS_AS X8*)(st + roff[kk]), kreg[kk], s);
+      dp = mfma32(*(const LDS_AS X8*)(st + R_B + roff[kk]), vreg[kk], dp);
     }
   };
 
-  if (n_t > 0) load_rows(t_begin, 0, rvo);
-  if (n_t > 1) load_rows(t_begin + 1, 1, rvo);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  // One loop per query half (wave-uniform branch outside the loops), so each
-  // phase's registers are live only in its own segment; both loops pass the
-  // same 2*n_t + 1 barriers. Segment 2i+1 (i >= 1) loads tile i+1 into the
-  // stage tile i-1 used.
-  auto seg_end = [&]() {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  };
-  if (qh == 0) {
-    for (int i = 0; i < n_t; ++i) {
-      const LDS_AS char* st = sm + OFF_R + (i & 1) * RS_B;
-      phase1(t_begin + i, st);  // segment 2i
-      seg_end();
-      if (i >= 1 && i + 1 < n_t) load_rows(t_begin + i + 1, (i + 1) & 1, rvo);  // segment 2i+1
-      phase2(st);
-      seg_end();
-    }
-    seg_end();  // segment 2*n_t: the other half's last phase 2
-  } else {
-    seg_end();  // segment 0: the other half's first phase 1
-    for (int i = 0; i < n_t; ++i) {
-      const LDS_AS char* st = sm + OFF_R + (i & 1) * RS_B;
-      if (i >= 1 && i + 1 < n_t) load_rows(t_begin + i + 1, (i + 1) & 1, rvo);  // segment 2i+1
-      phase1(t_begin + i, st);
-      seg_end();
-      phase2(st);  // segment 2i+2
-      seg_end();
+  f32x16 sa, da, sb, db;  // S / dP of the current and the next half
+  if (n_t > 0) scores(sm, 0, sa, da);
+  // Per tile: the second half's S/dP beside the first half's softmax, the
+  // first half's dV/dK; the next tile's first-half S/dP beside the second
+  // half's softmax (past the last tile they read a stale stage and are
+  // discarded), the second half's dV/dK; then the tile-end barrier: every
+  // wave is done with this stage, which takes the tile NST ahead, and the
+  // tile loaded at the previous barrier has landed.
+  for (int t0 = 0; t0 < n_t; t0 += NST) {
+#pragma unroll
+    for (int si = 0; si < NST; ++si) {
+      const int t = t0 + si;
+      if (t >= n_t) break;
+      const LDS_AS char* stg = sm + si * RS_B;
+      const LDS_AS char* nstg = sm + ((si + 1) % NST) * RS_B;
+      phase_x(stg, 1, sb, db, stg, t, 0, sa, da);
+      phase_y(stg, 0, sa, da);
+      phase_x(nstg, 0, sa, da, stg, t, 1, sb, db);
+      phase_y(stg, 1, sb, db);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (t + NST < n_t) load_tile(t_begin + t + NST, si, rvo);
     }
   }
 
-  // Sum the two query halves through LDS (f32x4 groups, lane-contiguous).
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  LDS_AS f32x4* park = (LDS_AS f32x4*)sm + kb * NG * 64 + lane;
-  if (qh == 1) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        park[(dt * 4 + g) * 64] = f32x4{dk[dt][4 * g], dk[dt][4 * g + 1], dk[dt][4 * g + 2], dk[dt][4 * g + 3]};
-        park[(DT * 4 + dt * 4 + g) * 64] = f32x4{dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3]};
-      }
-  }
-  __syncthreads();
-  if (qh == 0 && kcol < nk) {
+  if (kcol < nk) {
     T* rk = (T*)p.dk + (int64_t)b * p.sdkb + (int64_t)h * p.sdkh + (int64_t)kcol * p.sdkn;
     T* rv = (T*)p.dv + (int64_t)b * p.sdvb + (int64_t)h * p.sdvh + (int64_t)kcol * p.sdvn;
     const float sc = p.scale;
@@ -512,13 +580,11 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
       for (int g = 0; g < 4; ++g) {
         const int d = 32 * dt + 8 * g + 4 * hh;
         if (d < D) {
-          const f32x4 ok = park[(dt * 4 + g) * 64];
-          const f32x4 ov = park[(DT * 4 + dt * 4 + g) * 64];
           X4 ck, cv;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            ck[e] = (T)((dk[dt][4 * g + e] + ok[e]) * sc);
-            cv[e] = (T)(dv[dt][4 * g + e] + ov[e]);
+            ck[e] = (T)(dk[dt][4 * g + e] * sc);
+            cv[e] = (T)dv[dt][4 * g + e];
           }
           *(X4*)(rk + d) = ck;
           *(X4*)(rv + d) = cv;
@@ -541,7 +607,7 @@ static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
   }
   p.num_tiles = (p.Nk + 127) / 128;
   if ((phases & 2) && p.num_tiles > 0) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(512), 0, s, p);
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(256), 0, s, p);
     e = hipGetLastError();
   }
   return e;
