@@ -861,19 +861,27 @@ def main():
     # Per-kernel launch times on the launch stream (HIP events around
     # back-to-back launches): the forward from the timed steps; the backward's
     # two kernels one at a time through lsfa_bwd's phase flags (the dK/dV
-    # phase reuses the workspace the dQ phase just wrote).
-    kernels = [{"kernel": "fa_fwd_kernel", "flops_per_launch": f_fwd, "mfma_flops_per_launch": f_fwd,
-                "avg_launch_ms": fwd_avg}]
+    # phase reuses the workspace the dQ phase just wrote). The opt-in
+    # stored-dS backward (LSFA_BWD_STORED_DS: dK/dV kernel storing dS, then a
+    # dQ GEMM over it) is timed the same way, whole and per phase, and
+    # reported beside the default; its dQ GEMM moves dS once, so it is priced
+    # against HBM bandwidth (algorithmic bytes: the visible dS entries, 2
+    # bytes each, plus K and dQ).
+    kernels = [{"kernel": "fa_fwd_kernel", "bound": "mfma", "flops_per_launch": f_fwd,
+                "mfma_flops_per_launch": f_fwd, "avg_launch_ms": fwd_avg}]
+    stored_ds = None
     if bwd is not None:
         from lightserve_amd.kernels.flash_attention_backward import _backward_args
         from lightserve_amd import _lib as lib
         o_t, lse_t = fwd()
-        ba, keep = _backward_args(inp["do"], q, k, v, o_t, lse_t, inp["causal"])
         raw = stream.cuda_stream
         unit = f_fwd / 2  # one B*H*N^2*D GEMM (halved when causal)
-        for flag, name, alg_units, mfma_units in ((lib.BWD_ONLY_DQ, "fa_bwd_dq_kernel", 1, 3),
-                                                  (lib.BWD_ONLY_DKDV, "fa_bwd_dkdv_kernel", 4, 4)):
-            ba.flags = flag
+        Bq, Hq, Nq, Dq = q.shape
+        pairs = Nq * (Nq + 1) // 2 if inp["causal"] else Nq * Nq
+        dq_bytes = Bq * Hq * (2 * pairs + 2 * 2 * Nq * Dq)
+
+        def time_flags(ba, flags):
+            ba.flags = flags
             for _ in range(2):
                 lib.bwd(ba, raw)
             k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -883,10 +891,25 @@ def main():
                 lib.bwd(ba, raw)
             k1.record(stream)
             torch.cuda.synchronize()
-            kernels.append({"kernel": name, "flops_per_launch": alg_units * unit,
-                            "mfma_flops_per_launch": mfma_units * unit,
-                            "avg_launch_ms": k0.elapsed_time(k1) / args.steps})
+            return k0.elapsed_time(k1) / args.steps
+
+        ba, keep = _backward_args(inp["do"], q, k, v, o_t, lse_t, inp["causal"])
+        for flag, name, alg_units, mfma_units in ((lib.BWD_ONLY_DQ, "fa_bwd_dq_kernel", 1, 3),
+                                                  (lib.BWD_ONLY_DKDV, "fa_bwd_dkdv_kernel", 4, 4)):
+            kernels.append({"kernel": name, "bound": "mfma", "flops_per_launch": alg_units * unit,
+                            "mfma_flops_per_launch": mfma_units * unit, "avg_launch_ms": time_flags(ba, flag)})
         del keep
+        if Dq > 64 and q.dtype != torch.float32:
+            ba, keep = _backward_args(inp["do"], q, k, v, o_t, lse_t, inp["causal"], flags=lib.BWD_STORED_DS)
+            sd = lib.BWD_STORED_DS
+            stored_ds = {"flag": "LSFA_BWD_STORED_DS", "workspace_bytes": int(ba.workspace_bytes),
+                         "ms": round(time_flags(ba, sd), 5),
+                         "dkdv_phase_ms": round(time_flags(ba, sd | lib.BWD_ONLY_DKDV), 5),
+                         "dq_gemm_ms": round(time_flags(ba, sd | lib.BWD_ONLY_DQ), 5),
+                         "dq_gemm_bytes": dq_bytes}
+            stored_ds["dq_gemm_gbs"] = round(dq_bytes / (stored_ds["dq_gemm_ms"] * 1e-3) / 1e9, 1)
+            stored_ds["dq_gemm_hbm_frac"] = round(stored_ds["dq_gemm_gbs"] / HBM_PEAK_GBS, 4)
+            del keep
     for kd in kernels:
         kd["achieved"] = round(kd["flops_per_launch"] / (kd["avg_launch_ms"] * 1e-3) / 1e12, 2)
         kd["frac"] = round(kd["achieved"] / PEAK_BF16_TFLOPS, 4)
@@ -935,6 +958,9 @@ def main():
         result["bwd"] = {"tflops": round(fb / (bwd_avg * 1e-3) / 1e12, 2), "ms": round(bwd_avg, 5),
                          "pct_of_peak": round(100 * fb / (bwd_avg * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
                          "kernels": "fa_bwd_dq_kernel + fa_bwd_dkdv_kernel"}
+        if stored_ds is not None:
+            stored_ds["tflops"] = round(fb / (stored_ds["ms"] * 1e-3) / 1e12, 2)
+            result["bwd"]["stored_ds"] = stored_ds
         result["fwd_bwd"] = {"tflops": round(value, 2), "ms": round(ms_per_step, 5),
                              "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2)}
     if not args.no_cpu_baseline:

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define LSFA_ABI_VERSION 8
+#define LSFA_ABI_VERSION 9
 
 typedef enum {
   LSFA_DTYPE_FP32 = 0,
@@ -87,12 +87,18 @@ typedef struct {
 
 /* Backward arguments. workspace is caller-allocated device memory of at
  * least lsfa_bwd_workspace_size() bytes, 256-byte aligned; its contents on
- * entry do not matter and are scratch afterwards. The dq kernel's prologue
- * writes there what the reference's preprocess kernel computes (delta =
- * rowsum(dO * O), kernels/flash_attention_backward.py:202-229) and
- * L*log2(e) for the key-stationary kernel. dq/dk/dv
- * are written in the input dtype (no fp32 dq staging buffer and no atomics:
- * dq is produced by its own query-stationary kernel, so results are
+ * entry do not matter and are scratch afterwards. It receives what the
+ * reference's preprocess kernel computes (delta = rowsum(dO * O),
+ * kernels/flash_attention_backward.py:202-229) with L*log2(e) per query row.
+ * By default a query-stationary kernel produces dq and a key-stationary one
+ * dk and dv, each computing S and dP itself. With LSFA_BWD_STORED_DS (bf16 /
+ * fp16 at head_dim above 64) the key-stationary kernel also stores dS (in
+ * the input dtype) into the workspace and dq = scale * dS K is a GEMM over
+ * the stored values, so S and dP are computed once per (query, key): the
+ * dS region is (seqlen_k rounded up to 32) x (seqlen_q rounded up to 256)
+ * elements per head for as many heads as fit in 4 GiB (at least one), and
+ * larger problems run chunk by chunk. dq/dk/dv are written in the input
+ * dtype (no fp32 dq staging buffer and no atomics, so results are
  * deterministic). */
 typedef struct {
   const void* q;
@@ -126,18 +132,27 @@ typedef struct {
   int32_t head_dim;
   int32_t causal;
   float sm_scale;
-  int32_t flags;               /* 0 (both kernels) or one LSFA_BWD_ONLY_* phase */
+  int32_t flags;               /* 0, or LSFA_BWD_ONLY_* and / or LSFA_BWD_STORED_DS */
 } lsfa_bwd_args;
 
-/* lsfa_bwd_args.flags, for timing the two kernels of a bf16/fp16 backward
- * one at a time (a profiler or benchmark; 0 runs both, in order):
- * LSFA_BWD_ONLY_DQ runs the query-stationary kernel alone (it writes dq and
- * the workspace's per-row (L*log2(e), delta)); LSFA_BWD_ONLY_DKDV runs the
- * key-stationary kernel alone and reads those workspace values, so it needs
- * a workspace that an earlier full or ONLY_DQ call with the same arguments
- * filled. The fp32 path takes only 0. */
+/* lsfa_bwd_args.flags: at most one LSFA_BWD_ONLY_* phase, for timing the
+ * kernels of a bf16/fp16 backward one at a time (a profiler or benchmark;
+ * without one every kernel runs, in order), optionally with
+ * LSFA_BWD_STORED_DS.
+ * Default path: LSFA_BWD_ONLY_DQ runs the query-stationary kernel alone (it
+ * writes dq and the per-row values); LSFA_BWD_ONLY_DKDV runs the
+ * key-stationary kernel alone and reads those values, so it needs a
+ * workspace that an earlier full or ONLY_DQ call filled.
+ * Stored-dS path (LSFA_BWD_STORED_DS at head_dim above 64; the flag is
+ * ignored elsewhere): LSFA_BWD_ONLY_DKDV runs the per-row preprocess and the
+ * key-stationary kernel (dk, dv, and dS into the workspace);
+ * LSFA_BWD_ONLY_DQ runs the dq GEMM alone over the dS that an earlier full
+ * or ONLY_DKDV call with the same arguments and workspace left (problems
+ * that run in more than one chunk of heads take no ONLY_* flag).
+ * The fp32 path takes no ONLY_* flag. */
 #define LSFA_BWD_ONLY_DQ 1
 #define LSFA_BWD_ONLY_DKDV 2
+#define LSFA_BWD_STORED_DS 4
 
 /* Paged-KV decode arguments: one new query token per sequence against a KV
  * cache addressed through block tables. The reference has no such kernel;
@@ -444,11 +459,11 @@ int lsfa_fwd(const lsfa_fwd_args* args, void* stream);
 /* Host-only validation of backward arguments; never touches the GPU. */
 int lsfa_bwd_check(const lsfa_bwd_args* args);
 
-/* Workspace bytes lsfa_bwd needs for these arguments (only dtype, batch,
- * heads_q, seqlen_q and head_dim matter); no GPU work. */
+/* Workspace bytes lsfa_bwd needs for these arguments (only dtype, flags,
+ * batch, heads_q, seqlen_q and seqlen_k matter); no GPU work. */
 int lsfa_bwd_workspace_size(const lsfa_bwd_args* args, uint64_t* bytes);
 
-/* Backward: delta, then dq, dk, dv. Replaces the preprocess launch
+/* Backward: delta, then dk, dv and dq. Replaces the preprocess launch
  * (kernels/flash_attention_backward.py:341-350), the backward launch
  * (:363-381) and the fp32->dtype cast of dq (:382). */
 int lsfa_bwd(const lsfa_bwd_args* args, void* stream);
@@ -456,11 +471,12 @@ int lsfa_bwd(const lsfa_bwd_args* args, void* stream);
 /* Allocation-free backward. No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * training or serving loops that forbid allocation). Same arguments, kernels
- * and results as lsfa_bwd, except that workspace and workspace_bytes are
- * ignored: the workspace is a device array of LSFA_BWD_SCRATCH_BYTES inside
- * the library (one per GPU, held while the library is loaded), so problems
- * needing more (lsfa_bwd_workspace_size above that: batch * heads_q *
- * seqlen_q rounded up to 128 above 2097152 rows) are rejected with
+ * and results as lsfa_bwd with LSFA_BWD_STORED_DS cleared from flags (the
+ * default kernels need only the per-row values), except that workspace and
+ * workspace_bytes are ignored: the workspace is a device array of
+ * LSFA_BWD_SCRATCH_BYTES inside the library (one per GPU, held while the
+ * library is loaded), so problems needing more (batch * heads_q * seqlen_q
+ * rounded up to 128 above 2097152 rows) are rejected with
  * LSFA_ERR_UNSUPPORTED. Calls share their GPU's array: two calls that can run
  * at the same time on one GPU (different streams) race; calls in stream order
  * do not. Nothing in the array needs clearing between calls (each call

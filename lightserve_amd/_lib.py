@@ -13,9 +13,10 @@ import torch
 
 _LIB_NAME = "liblsfa_gfx950.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 8
+ABI_VERSION = 9
 BWD_SCRATCH_BYTES = 16777216  # LSFA_BWD_SCRATCH_BYTES: lsfa_bwd_noalloc's workspace limit
-BWD_ONLY_DQ, BWD_ONLY_DKDV = 1, 2  # lsfa_bwd_args.flags: run one backward kernel (timing)
+BWD_ONLY_DQ, BWD_ONLY_DKDV = 1, 2  # lsfa_bwd_args.flags: run one backward phase (timing)
+BWD_STORED_DS = 4  # lsfa_bwd_args.flags: dk/dv kernel stores dS, dq is a GEMM over it (head_dim > 64)
 
 DTYPE_FP32, DTYPE_FP16, DTYPE_BF16 = 0, 1, 2
 TORCH_TO_LSFA = {torch.float32: DTYPE_FP32, torch.float16: DTYPE_FP16, torch.bfloat16: DTYPE_BF16}

@@ -83,23 +83,50 @@ int check_common(int dtype, int batch, int hq, int hkv, int nq, int nk, int d, f
 }
 
 // Backward workspace: (lse*log2e, delta) pairs for every (b, h, query),
-// queries padded to a multiple of the query-stationary tile (128, which the
-// dq kernel writes whole).
+// queries padded to a multiple of 128 (the recompute path's dq kernel writes
+// whole 128-row tiles). The stored-dS path (LSFA_BWD_STORED_DS, bf16/fp16
+// with head_dim above 64) adds, 256-byte aligned, dS of a chunk of heads in
+// the input dtype: per head ceil(seqlen_k / 32) rows of ds_ldq / 32 blocks
+// of 32 keys x 32 queries (1024 elements), ds_ldq = seqlen_q rounded up to
+// the dQ kernel's 256-query tile. A chunk is as many heads as fit in
+// kDsChunkBytes (at least one); the backward then runs chunk by chunk. At
+// head_dim <= 64 moving dS through HBM costs more than recomputing it, so
+// the flag does not apply there.
 struct BwdWorkspace {
   int64_t nq_pad = 0;
   uint64_t ld_off = 0, bytes = 0;
+  bool stored_ds = false;
+  uint64_t ds_off = 0;
+  int64_t ds_ldq = 0, ds_sbh = 0;
+  int chunk_heads = 0, chunks = 0;
 };
+
+constexpr uint64_t kDsChunkBytes = uint64_t(4) << 30;
 
 uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
-BwdWorkspace bwd_workspace(int dtype, int batch, int heads, int nq, int head_dim) {
-  (void)dtype;
-  (void)head_dim;
+bool bwd_stored_ds(int dtype, int flags, int head_dim) {
+  return dtype != LSFA_DTYPE_FP32 && (flags & LSFA_BWD_STORED_DS) != 0 && padded_dim(head_dim) == 128;
+}
+
+BwdWorkspace bwd_workspace(int dtype, int flags, int batch, int heads, int nq, int nk, int head_dim) {
   BwdWorkspace w;
   w.nq_pad = ((int64_t)nq + 127) / 128 * 128;
   const uint64_t rows = (uint64_t)batch * heads * w.nq_pad;
   w.ld_off = 0;
   w.bytes = align256(rows * 8);
+  const int64_t bh = (int64_t)batch * heads;
+  if (bwd_stored_ds(dtype, flags, head_dim) && bh > 0 && nq > 0 && nk > 0) {
+    w.stored_ds = true;
+    w.ds_ldq = ((int64_t)nq + 255) / 256 * 256;
+    w.ds_sbh = ((int64_t)nk + 31) / 32 * 32 * w.ds_ldq;
+    const uint64_t head_bytes = (uint64_t)w.ds_sbh * 2;
+    const uint64_t fit = kDsChunkBytes / head_bytes;
+    w.chunk_heads = (int)(fit < 1 ? 1 : (fit > (uint64_t)bh ? bh : fit));
+    w.chunks = (int)((bh + w.chunk_heads - 1) / w.chunk_heads);
+    w.ds_off = w.bytes;
+    w.bytes = w.ds_off + align256(head_bytes * w.chunk_heads);
+  }
   return w;
 }
 
@@ -222,15 +249,21 @@ int lsfa_bwd_check(const lsfa_bwd_args* a) {
   if (a->cu_seqlens_q != nullptr || a->cu_seqlens_k != nullptr)
     return fail(LSFA_ERR_UNSUPPORTED, "varlen backward is not implemented");
   if (a->heads_kv != a->heads_q) return fail(LSFA_ERR_UNSUPPORTED, "GQA backward is not implemented (heads_kv != heads_q)");
-  if (a->flags != 0 && a->flags != LSFA_BWD_ONLY_DQ && a->flags != LSFA_BWD_ONLY_DKDV)
+  const int phase = a->flags & ~LSFA_BWD_STORED_DS;
+  if (phase != 0 && phase != LSFA_BWD_ONLY_DQ && phase != LSFA_BWD_ONLY_DKDV)
     return fail(LSFA_ERR_INVALID, "unknown flags %d", a->flags);
-  if (a->flags != 0 && a->dtype == LSFA_DTYPE_FP32)
-    return fail(LSFA_ERR_UNSUPPORTED, "the fp32 backward runs both phases together (flags must be 0)");
+  if (phase != 0 && a->dtype == LSFA_DTYPE_FP32)
+    return fail(LSFA_ERR_UNSUPPORTED, "the fp32 backward runs both phases together (no LSFA_BWD_ONLY_* flag)");
   const bool empty = (long long)a->batch * a->heads_q * (a->seqlen_q + a->seqlen_k) == 0;
   if (!empty) {
     if (!a->q || !a->k || !a->v || !a->o || !a->dout || !a->lse || !a->dq || !a->dk || !a->dv)
       return fail(LSFA_ERR_INVALID, "q, k, v, o, dout, lse, dq, dk and dv must be non-NULL");
-    const BwdWorkspace w = bwd_workspace(a->dtype, a->batch, a->heads_q, a->seqlen_q, a->head_dim);
+    const BwdWorkspace w = bwd_workspace(a->dtype, a->flags, a->batch, a->heads_q, a->seqlen_q, a->seqlen_k, a->head_dim);
+    if (phase != 0 && w.chunks > 1)
+      return fail(LSFA_ERR_UNSUPPORTED,
+                  "LSFA_BWD_ONLY_* with LSFA_BWD_STORED_DS needs the stored dS of all heads at once (this "
+                  "problem runs in %d chunks)",
+                  w.chunks);
     if (w.bytes > 0 && !a->workspace) return fail(LSFA_ERR_INVALID, "workspace must be non-NULL");
     if (a->workspace_bytes < w.bytes)
       return fail(LSFA_ERR_INVALID, "workspace_bytes %llu is below the %llu bytes lsfa_bwd_workspace_size asks for",
@@ -255,7 +288,7 @@ int lsfa_bwd_workspace_size(const lsfa_bwd_args* a, uint64_t* bytes) {
   if (a == nullptr || bytes == nullptr) return fail(LSFA_ERR_INVALID, "args or bytes is NULL");
   int rc = check_common(a->dtype, a->batch, a->heads_q, a->heads_kv, a->seqlen_q, a->seqlen_k, a->head_dim, a->sm_scale);
   if (rc) return rc;
-  *bytes = bwd_workspace(a->dtype, a->batch, a->heads_q, a->seqlen_q, a->head_dim).bytes;
+  *bytes = bwd_workspace(a->dtype, a->flags, a->batch, a->heads_q, a->seqlen_q, a->seqlen_k, a->head_dim).bytes;
   return ok();
 }
 
@@ -266,12 +299,18 @@ static int run_bwd(const lsfa_bwd_args* a, void* stream) {
   memset(&p, 0, sizeof(p));
   p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.dout = a->dout; p.lse = a->lse;
   p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
-  const BwdWorkspace w = bwd_workspace(a->dtype, a->batch, a->heads_q, a->seqlen_q, a->head_dim);
+  const BwdWorkspace w = bwd_workspace(a->dtype, a->flags, a->batch, a->heads_q, a->seqlen_q, a->seqlen_k, a->head_dim);
   char* ws = static_cast<char*>(a->workspace);
   p.nq_pad = (int)w.nq_pad;
   p.ld = reinterpret_cast<float*>(ws + w.ld_off);
   p.sldh = 2 * w.nq_pad;
   p.sldb = (int64_t)a->heads_q * p.sldh;
+  if (w.stored_ds) {
+    p.ds = ws + w.ds_off;
+    p.ds_ldq = w.ds_ldq;
+    p.ds_sbh = w.ds_sbh;
+    p.nbh = w.chunk_heads;
+  }
   p.sqb = a->q_stride[0]; p.sqh = a->q_stride[1]; p.sqn = a->q_stride[2]; p.sqd = a->q_stride[3];
   p.skb = a->k_stride[0]; p.skh = a->k_stride[1]; p.skn = a->k_stride[2]; p.skd = a->k_stride[3];
   p.svb = a->v_stride[0]; p.svh = a->v_stride[1]; p.svn = a->v_stride[2]; p.svd = a->v_stride[3];
@@ -290,8 +329,11 @@ static int run_bwd(const lsfa_bwd_args* a, void* stream) {
   if (a->dtype == LSFA_DTYPE_FP32)
     e = lsfa::bwd_f32(p, dp, a->causal != 0, s);
   else
+  {
+    const int phase = a->flags & ~LSFA_BWD_STORED_DS;
     e = lsfa::bwd_mfma(p, a->dtype == LSFA_DTYPE_BF16, dp, a->causal != 0,
-                       a->flags == LSFA_BWD_ONLY_DQ ? 1 : (a->flags == LSFA_BWD_ONLY_DKDV ? 2 : 3), s);
+                       phase == LSFA_BWD_ONLY_DQ ? 1 : (phase == LSFA_BWD_ONLY_DKDV ? 2 : 3), s);
+  }
   if (e != hipSuccess) return fail(LSFA_ERR_LAUNCH, "backward launch failed: %s", hipGetErrorString(e));
   return ok();
 }
@@ -332,8 +374,12 @@ int scratch_for_current_device(void** out) {
 }
 }  // namespace
 
-int lsfa_bwd_noalloc(const lsfa_bwd_args* a, void* stream) {
-  if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+int lsfa_bwd_noalloc(const lsfa_bwd_args* args, void* stream) {
+  if (args == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
+  // The recompute kernels: their workspace is the per-row pairs alone.
+  lsfa_bwd_args r = *args;
+  r.flags &= ~LSFA_BWD_STORED_DS;
+  const lsfa_bwd_args* a = &r;
   uint64_t need = 0;
   int rc = lsfa_bwd_workspace_size(a, &need);
   if (rc) return rc;

@@ -10,6 +10,7 @@
 //
 // Unlike the reference (one key-stationary kernel with fp32 atomic adds into
 // a dq workspace, :323-325, followed by a cast, :382), the work is split into
+// two kernels; by default
 //   fa_bwd_dq_kernel   : query-stationary. Its prologue does the reference's
 //                        preprocess (:341-350): delta and L*log2(e) per query
 //                        row into the workspace. Then dQ = scale * dS K over
@@ -17,13 +18,19 @@
 //                        dtype;
 //   fa_bwd_dkdv_kernel : key-stationary; dK, dV over all visible query tiles
 //                        (runs after the dq kernel, which feeds it).
-// Both kernels recompute S and dP. There are no atomics and no fp32 dq
-// buffer, so results are deterministic.
+// Both kernels recompute S and dP. The stored-dS path instead runs
+//   fa_bwd_prep_kernel : the preprocess (delta, L*log2(e)) on its own;
+//   fa_bwd_dkdv_kernel<..., DS = true> : as above, also storing dS;
+//   fa_bwd_dq_ds_kernel : dQ = scale * dS K over the stored dS,
+// which computes S and dP once but moves dS through HBM twice.
+// There are no atomics and no fp32 dq buffer, so results are deterministic.
 #include "fa_common.hpp"
 
 namespace lsfa {
 
 constexpr float kLog2eB = 1.4426950408889634f;
+// Cache-policy operand of the buffer builtins: the non-temporal (streaming) hint.
+constexpr int kCacheNT = 2;
 
 // ---------------------------------------------------------------------------
 // dQ. Workgroup = 4 waves x 32 query rows, at most 256 registers
@@ -272,10 +279,19 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 // A tile's stage is refilled after every wave has finished its second half
 // (one barrier per tile); a tile is loaded three halves-iterations before its
 // first use. Query rows beyond the sequence have L = +inf in the workspace
-// (written by the dq kernel's prologue), so their P is exactly 0; head-dim
-// columns at or past D load as zero. dK is scaled by sm_scale at the end.
+// (written by the dq kernel's prologue or the preprocess kernel), so their P
+// is exactly 0; head-dim columns at or past D load as zero. dK is scaled by
+// sm_scale at the end.
+// With DS, the wave also stores dS (in the input dtype: the exact values its
+// dK MFMAs take) for fa_bwd_dq_ds_kernel, as 2 KB blocks of 32 keys x 32
+// queries in register order: a half's G0 words of all 64 lanes fill the
+// block's first KB, its G1 words the second, lane l's 16 bytes at unit
+// l ^ 8 (l / 32) (^ 4 in the second KB) so that the reader's transpose reads
+// spread over all LDS banks. Each store instruction writes 1 KB of
+// contiguous memory. Keys at or past nk are stored as zero, masked (causal)
+// entries are zero already.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, bool CAUSAL>
+template <typename T, int DP, bool CAUSAL, bool DS>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
@@ -298,6 +314,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   const bool w_hi = wave >= NW / 2;  // waves 2, 3 load dO; 0, 1 load Q
   int bh, kt;
   map_tile(p.num_tiles, gridDim.x, bh, kt, false);  // low key tiles see the most queries
+  bh += p.bh0;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nq = p.Nq, nk = p.Nk, D = p.D;
   const int k0 = kt * BNK;
@@ -314,6 +331,27 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   if (CAUSAL) t_begin = max(0, k0 - off) / BMQ;  // first tile holding a query that sees key k0
   const int n_t = max(0, n_qt - t_begin);
   const int kcol = k0 + 32 * kb + l32;  // this lane's key
+
+  // dS blocks: this wave's 32 keys are block row kblk of the head, blocks
+  // [kblk][query / 32] of 1024 elements; a wave with no key below nk stores
+  // nothing (empty descriptor).
+  __amdgpu_buffer_rsrc_t dsr;
+  int dso0 = 0, dso1 = 0;
+  if constexpr (DS) {
+    const int nqb = (int)(p.ds_ldq >> 5);
+    const T* base = (const T*)p.ds + (int64_t)(bh - p.bh0) * p.ds_sbh + (int64_t)((k0 >> 5) + kb) * nqb * 1024;
+    dsr = tile_rsrc(base, k0 + 32 * kb < nk ? nqb * 2048 : 0);
+    dso0 = 16 * (lane ^ (8 * hh));
+    dso1 = 1024 + 16 * (lane ^ (8 * hh) ^ 4);
+  }
+  // The G0 (g = 0) or G1 (g = 1) words of the half whose first query is qfirst.
+  auto store_ds = [&](int qfirst, const u32x4& w, int g) {
+    if constexpr (DS) {
+      const u32x4 v = kcol < nk ? w : u32x4{0u, 0u, 0u, 0u};
+      // nt: dS is read once, by another kernel, long after it leaves L2
+      __builtin_amdgcn_raw_buffer_store_b128(v, dsr, (qfirst >> 5) * 2048 + (g ? dso1 : dso0), 0, kCacheNT);
+    }
+  };
 
   // Row-major tile loads (see fa_bwd_dq_kernel's row_voff).
   auto row_voff = [&](int lc, int64_t sn) -> int {
@@ -494,8 +532,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     }
     P0 = __builtin_bit_cast(X8, p0w);
     G0 = __builtin_bit_cast(X8, g0w);
+    store_ds(q0, g0w, 0);
   };
-  auto phase_y = [&](const LDS_AS char* stg, int q, const f32x16& s, const f32x16& dp) {
+  auto phase_y = [&](const LDS_AS char* stg, int t, int q, const f32x16& s, const f32x16& dp) {
     const LDS_AS char* st = stg + 32 * q * DP * 2;
     // MFMA c: ks = c / (2 DT), dt = (c / 2) % DT; even c is dV (dO^T), odd c dK (Q^T)
     auto opread = [&](int c) -> X8 {
@@ -521,6 +560,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
         if (c == 2 * DT - 1) {
           P1 = __builtin_bit_cast(X8, p1w);
           G1 = __builtin_bit_cast(X8, g1w);
+          store_ds((t_begin + t) * BMQ + 32 * q, g1w, 1);
         }
       }
       const int dt = (c >> 1) % DT, ks = c / (2 * DT);
@@ -561,9 +601,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
       const LDS_AS char* stg = sm + si * RS_B;
       const LDS_AS char* nstg = sm + ((si + 1) % NST) * RS_B;
       phase_x(stg, 1, sb, db, stg, t, 0, sa, da);
-      phase_y(stg, 0, sa, da);
+      phase_y(stg, t, 0, sa, da);
       phase_x(nstg, 0, sa, da, stg, t, 1, sb, db);
-      phase_y(stg, 1, sb, db);
+      phase_y(stg, t, 1, sb, db);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (t + NST < n_t) load_tile(t_begin + t + NST, si, rvo);
@@ -593,21 +633,299 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   }
 }
 
-// phases: bit 0 the dq kernel, bit 1 the dk/dv kernel.
+// ---------------------------------------------------------------------------
+// Preprocess of the stored-dS path (kernels/flash_attention_backward.py:
+// 341-350): per query row delta = rowsum(dO * O) (products of the input-dtype
+// values in fp32) and L * log2(e) into the ld workspace; rows Nq .. nq_pad-1
+// and rows whose L is -inf get (+inf, 0), so that their P is exactly 0.
+// Block = 64 rows x 4 lanes; lane part of a row sums the 16-byte chunks
+// part, part + 4, ... of both rows.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void fa_bwd_prep_kernel(const BwdParams p) {
+  using X8 = typename VecT<T>::x8;
+  constexpr int LPR = 4, RPB = 256 / LPR;
+  constexpr int CH = (DP / 8 + LPR - 1) / LPR;
+  const int tiles = p.nq_pad / RPB;
+  const int bh = blockIdx.x / tiles, rt = blockIdx.x - bh * tiles;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int row = rt * RPB + (int)threadIdx.x / LPR, part = threadIdx.x % LPR;
+  float acc = 0.f, l2 = INFINITY;
+  if (row < p.Nq) {
+    const T* orow = (const T*)p.o + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)row * p.son;
+    const T* drow = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh + (int64_t)row * p.sdon;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int col = 8 * (c * LPR + part);
+      if (col < p.D) {
+        const X8 ov = __builtin_bit_cast(X8, ldg16(orow + col));
+        const X8 dv = __builtin_bit_cast(X8, ldg16(drow + col));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)dv[e] * (float)ov[e];
+      }
+    }
+    const float lse = p.lse[(int64_t)b * p.slb + (int64_t)h * p.slh + (int64_t)row * p.sln];
+    if (lse != -INFINITY) l2 = lse * kLog2eB;
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  if (part == 0) {
+    float2 v;
+    v.x = l2;
+    v.y = acc;
+    *(float2*)(p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 2 * (int64_t)row) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ of the stored-dS path: dQ = scale * dS K, a GEMM over the dS blocks that
+// fa_bwd_dkdv_kernel<..., DS> stored, so S and dP are not computed a second
+// time. Workgroup = 8 waves x 32 query rows (256 queries of one (batch,
+// head)); key tiles of 64 go global -> LDS by direct buffer loads through NST
+// stages: the tile's 16 dS blocks (2 block rows x 8 query blocks, each block
+// row 16 KB of contiguous memory) and the K tile [64][DP]. Per tile and wave
+// (wave w owns query block w):
+//   dQ^T += K^T dS^T   A = K^T (transpose reads of K rows), B = dS^T
+// with the 16-key MFMA steps in natural key order: lane l of the B operand
+// needs keys 8 (l / 32) + 0..7 of query l % 32, and each 8-byte piece of a
+// block holds 4 consecutive queries of one key, so a transpose read of 4
+// pieces (4 keys) per 16-lane group delivers them. Keys at or past nk are
+// zero (stored so, and K rows past nk load as zero). Causal: a wave skips
+// the tiles wholly above its diagonal, and zeroes the dS entries with
+// key > query + (Nk - Nq) in the tiles it crosses (there the dK/dV kernel
+// stored zeros or, in blocks left of its first query tile, nothing).
+// ---------------------------------------------------------------------------
+template <typename T, int DP, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void fa_bwd_dq_ds_kernel(const BwdParams p) {
+  using X8 = typename VecT<T>::x8;
+  using X4 = typename VecT<T>::x4;
+  constexpr int NW = 8, BM = NW * 32, BN = 64, NST = 3;
+  constexpr int DS_B = BN * BM * 2;           // dS bytes of a tile (16 blocks)
+  constexpr int K_B = BN * DP * 2;            // K tile bytes
+  constexpr int STG_B = DS_B + K_B;           // one stage
+  constexpr int NCH = STG_B / 1024;           // 1 KB load chunks per stage
+  constexpr int CPW = (NCH + NW - 1) / NW;    // chunk slots per wave
+  constexpr int DT = DP / 32;
+  static_assert(K_B % 1024 == 0, "K tile must be whole 1 KB chunks");
+  static_assert(NST * STG_B <= 160 * 1024, "LDS budget");
+
+  __shared__ __attribute__((aligned(1024))) char sm_raw[NST * STG_B];
+  LDS_AS char* sm = (LDS_AS char*)sm_raw;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = lane >> 5;
+  int bh, qt;
+  map_tile(p.num_tiles, gridDim.x, bh, qt, CAUSAL);
+  bh += p.bh0;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int nq = p.Nq, nk = p.Nk, D = p.D;
+  const int q0 = qt * BM;
+  const int off = nk - nq;
+  const int nqb = (int)(p.ds_ldq >> 5);  // query blocks per block row
+  const int nkb = (nk + 31) >> 5;        // block rows
+
+  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh;
+  const T* dS = (const T*)p.ds + (int64_t)(bh - p.bh0) * p.ds_sbh + (int64_t)(q0 >> 5) * 1024;
+  T* dQ = (T*)p.dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh;
+
+  const int qw_lo = q0 + wave * 32;
+  const int qrow = qw_lo + (lane & 31);
+
+  int kv_end = nk;
+  if (CAUSAL) kv_end = min(nk, q0 + BM + off);
+  const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+
+  // Chunk slot i of this wave is stage chunk c = wave + NW i: chunks
+  // 0 .. DS_B/1024 - 1 copy the two 16 KB block rows as they are (chunk c
+  // of the stage = KB c % 16 of block row c / 16), the rest fill the K tile
+  // (lane t writes the chunk's bytes [16 t, 16 t + 16), i.e. stored segment
+  // (byte % row) / 16 of a row, which holds logical segment stored ^
+  // seg_swz(row)).
+  int cvo[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int c = wave + NW * i;
+    if (c < DS_B / 1024) {
+      cvo[i] = (c >> 4) * nqb * 2048 + (c & 15) * 1024 + lane * 16;
+    } else {
+      const int byte = (c - DS_B / 1024) * 1024 + lane * 16;
+      const int row = byte / (DP * 2);
+      const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+      cvo[i] = seg * 8 < D ? (int)(row * p.skn * 2) + seg * 16 : (int)0x80000000;
+    }
+  }
+  // (the offsets come in as a pointer parameter: indexing the captured array
+  // itself in the builtin's argument makes clang's host pass drop the
+  // kernel's launch stub)
+  auto load_tile = [&](int j, int stage, const int* vo) {
+    const int rows = min(nk - j * BN, BN);
+    const int brows = min(nkb - 2 * j, 2);  // block rows of this tile below nk
+    const __amdgpu_buffer_rsrc_t rd =
+        tile_rsrc(dS + (int64_t)2 * j * nqb * 1024, (brows - 1) * nqb * 2048 + DS_B / 2);
+    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(K + (int64_t)j * BN * p.skn, (int)(rows * p.skn * 2));
+    LDS_AS char* dst = sm + stage * STG_B;
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const int c = wave + NW * i;
+      if (c < DS_B / 1024)  // dS streams through once: nt keeps it from displacing K in L2
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (LDS_AS void*)(dst + c * 1024), 16, vo[i], 0, 0, kCacheNT);
+      else if (c < NCH)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(dst + c * 1024), 16, vo[i], 0, 0, 0);
+    }
+  };
+
+  // Transpose-read offsets. Inside 16-lane group G (g = G % 2 picks the
+  // block's KB, i.e. queries 16 g .. 16 g + 15; hh = G / 2 the MFMA's key
+  // half), lane 4 j + r addresses the piece of key 8 hh + j (+ 4 for the
+  // second read) holding queries 16 g + 8 (r / 2) + 4 (r % 2) .. + 3: unit
+  // key + 32 (r % 2), swizzled as stored, byte 8 (r / 2) of it.
+  const int G = lane >> 4, jj = (lane & 15) >> 2, rr = lane & 3, gq = G & 1;
+  auto unit = [&](int key) { return (key + 32 * (rr & 1)) ^ (8 * (rr & 1)) ^ (4 * gq); };
+  const int dsb0 = wave * 2048 + gq * 1024 + 16 * unit(8 * hh + jj) + 8 * (rr >> 1);
+  const int dsb1 = wave * 2048 + gq * 1024 + 16 * unit(8 * hh + 4 + jj) + 8 * (rr >> 1);
+  // K^T in the same key order: rows 8 hh + j and 8 hh + 4 + j.
+  const int tr_row = 8 * hh + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int troff[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    troff[dt][0] = swz_off<DP>(tr_row, 32 * dt + tr_col) * 2;
+    troff[dt][1] = swz_off<DP>(tr_row + 4, 32 * dt + tr_col) * 2;
+  }
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i)
+    if (i < ntiles) load_tile(i, i, cvo);
+
+  for (int j0 = 0; j0 < ntiles; j0 += NST) {
+#pragma unroll
+    for (int si = 0; si < NST; ++si) {
+      const int j = j0 + si;
+      if (j >= ntiles) break;
+      // Tile j has landed once at most the next tile's loads are
+      // outstanding (loads complete in order; waves with one more chunk slot
+      // wait a little longer); then every wave is past tile j - 1, whose
+      // stage takes tile j + NST - 1.
+      if (j + 1 < ntiles)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCH / NW) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (j + NST - 1 < ntiles) load_tile(j + NST - 1, (si + NST - 1) % NST, cvo);
+      const int kbase = j * BN;
+      const bool active = !CAUSAL || (kbase <= qw_lo + 31 + off);
+      if (active) {
+        const LDS_AS char* st = sm + si * STG_B;
+        const LDS_AS char* kt = st + DS_B;
+        // slot s of the B operand is key kbase + 16 ks + 8 hh + s: masked if
+        // 16 ks + s > lim
+        const bool need_mask = CAUSAL && kbase + BN - 1 > qw_lo + off;
+        const int lim = qrow + off - kbase - 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < BN / 16; ++ks) {
+          const LDS_AS char* db = st + (ks >> 1) * (DS_B / 2) + (ks & 1) * 256;
+          X8 bop = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(db + dsb0)), lds_read_tr((const LDS_AS T*)(db + dsb1)));
+          if (need_mask) {
+            asm volatile("" ::: "memory");
+            u32x4 w = __builtin_bit_cast(u32x4, bop);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int k_lo = 16 * ks + 2 * e;
+              const uint32_t m = (k_lo > lim ? 0u : 0xffffu) | (k_lo + 1 > lim ? 0u : 0xffff0000u);
+              w[e] &= m;
+            }
+            bop = __builtin_bit_cast(X8, w);
+          }
+          const LDS_AS char* kb = kt + ks * 16 * DP * 2;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const X8 a = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(kb + troff[dt][0])),
+                                      lds_read_tr((const LDS_AS T*)(kb + troff[dt][1])));
+            acc[dt] = mfma32(a, bop, acc[dt]);
+          }
+        }
+      }
+    }
+  }
+
+  if (qrow < nq) {
+    T* row = dQ + (int64_t)qrow * p.sdqn;
+    const float sc = p.scale;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * dt + 8 * g + 4 * hh;
+        if (d < D) {
+          X4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (T)(acc[dt][4 * g + e] * sc);
+          *(X4*)(row + d) = v;
+        }
+      }
+    }
+  }
+}
+
+// Stored-dS path (head dim 128; phases: bit 0 dQ, bit 1 dK/dV):
+// fa_bwd_prep_kernel, then per chunk of p.nbh heads fa_bwd_dkdv_kernel
+// storing dS into p.ds and fa_bwd_dq_ds_kernel reading it back.
+template <typename T, bool CAUSAL>
+static hipError_t launch_bwd_ds(BwdParams p, int phases, hipStream_t s) {
+  hipError_t e = hipSuccess;
+  const int BH = p.B * p.H;
+  const int ktiles = (p.Nk + 127) / 128, qtiles = (p.Nq + 255) / 256;
+  if ((phases & 2) && p.nq_pad > 0) {
+    hipLaunchKernelGGL((fa_bwd_prep_kernel<T, 128>), dim3(BH * (p.nq_pad / 64)), dim3(256), 0, s, p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  for (int bh0 = 0; bh0 < BH; bh0 += p.nbh) {
+    BwdParams c = p;
+    c.bh0 = bh0;
+    const int n = BH - bh0 < p.nbh ? BH - bh0 : p.nbh;
+    if ((phases & 2) && ktiles > 0) {
+      c.num_tiles = ktiles;
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, 128, CAUSAL, true>), dim3(ktiles * n), dim3(256), 0, s, c);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if ((phases & 1) && qtiles > 0) {
+      c.num_tiles = qtiles;
+      hipLaunchKernelGGL((fa_bwd_dq_ds_kernel<T, 128, CAUSAL>), dim3(qtiles * n), dim3(512), 0, s, c);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+  }
+  return e;
+}
+
+// phases: bit 0 dQ, bit 1 dK/dV. With p.ds set, the stored-dS path above;
+// otherwise the recompute path: fa_bwd_dq_kernel (whose prologue writes the
+// ld pairs), then fa_bwd_dkdv_kernel.
 template <typename T, int DP, bool CAUSAL>
 static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
+  if (p.ds != nullptr) {
+    if constexpr (DP == 128) return launch_bwd_ds<T, CAUSAL>(p, phases, s);
+    return hipErrorInvalidValue;  // the host takes the stored-dS path only at head dim 128
+  }
   // An empty axis means an empty grid: that kernel has nothing to write
   // (with no queries dK = dV = 0 still needs the dK/dV kernel, which then
   // runs no query tile).
   hipError_t e = hipSuccess;
+  const int BH = p.B * p.H;
+  p.bh0 = 0;
+  p.nbh = BH;
   p.num_tiles = (p.Nq + 127) / 128;
   if ((phases & 1) && p.num_tiles > 0) {
-    hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   p.num_tiles = (p.Nk + 127) / 128;
   if ((phases & 2) && p.num_tiles > 0) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * p.B * p.H), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
     e = hipGetLastError();
   }
   return e;

@@ -179,6 +179,11 @@ struct BwdParams {
   float* ld;
   int64_t sldb, sldh;
   int nq_pad;  // Nq rounded up to the query-stationary tile (128)
+  // Stored-dS path: dS^T rows (input dtype) of heads bh0 .. bh0 + nbh - 1,
+  // element (key n, query m) of head bh at (bh - bh0) * ds_sbh + n * ds_ldq + m
+  void* ds;
+  int64_t ds_sbh, ds_ldq;
+  int bh0, nbh;
   int64_t sqb, sqh, sqn;
   int64_t skb, skh, skn;
   int64_t svb, svh, svn;

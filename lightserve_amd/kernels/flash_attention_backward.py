@@ -30,11 +30,11 @@ def _flash_attention_forward_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
 
 
 def _backward_args(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
-                   L: torch.Tensor, causal: bool, sm_scale=None):
+                   L: torch.Tensor, causal: bool, sm_scale=None, flags=0):
     """The lsfa_bwd arguments for these tensors, and what they point into:
     (args, keep) with keep = (dq, dk, dv, the kernel-layout outputs, the
     inputs' kernel-layout views or copies, workspace). None for an empty
-    problem."""
+    problem. flags: lsfa_bwd_args.flags (the workspace is sized for them)."""
     B, H, N, D = q.shape
     scale = default_scale(D, sm_scale)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
@@ -58,7 +58,7 @@ def _backward_args(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.
         dk_stride=_lib.strides4(dkk), dv_stride=_lib.strides4(dvk), lse_stride=_lib._i64x3(*L.stride()),
         cu_seqlens_q=None, cu_seqlens_k=None,
         dtype=_lib.TORCH_TO_LSFA[q.dtype], batch=B, heads_q=H, heads_kv=H, seqlen_q=N, seqlen_k=N,
-        head_dim=dp, causal=int(bool(causal)), sm_scale=scale, flags=0,
+        head_dim=dp, causal=int(bool(causal)), sm_scale=scale, flags=flags,
     )
     nbytes = _lib.bwd_workspace_size(args)
     # The caching allocator hands out 512-byte aligned blocks (the ABI asks for 256).

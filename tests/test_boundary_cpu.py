@@ -198,17 +198,23 @@ def test_abi_backward_validation(built_library):
     rc, msg = _lib.bwd_check(args)
     assert rc == -2 and "varlen" in msg
     args.cu_seqlens_q = args.cu_seqlens_k = None
-    # flags: 0 or one phase (LSFA_BWD_ONLY_DQ / ONLY_DKDV); the fp32 path takes only 0
-    for f in (_lib.BWD_ONLY_DQ, _lib.BWD_ONLY_DKDV):
+    # flags: at most one phase (LSFA_BWD_ONLY_DQ / ONLY_DKDV), with or without
+    # LSFA_BWD_STORED_DS; the fp32 path takes no phase (STORED_DS is ignored)
+    args.workspace_bytes = 1 << 40
+    for f in (_lib.BWD_ONLY_DQ, _lib.BWD_ONLY_DKDV, _lib.BWD_STORED_DS):
+        for r in (0, _lib.BWD_STORED_DS):
+            args.flags = f | r
+            assert _lib.bwd_check(args)[0] == 0, args.flags
+    for f in (3, 8, 3 | _lib.BWD_STORED_DS, -1):
         args.flags = f
-        assert _lib.bwd_check(args)[0] == 0
-    args.flags = 3
-    rc, msg = _lib.bwd_check(args)
-    assert rc == -1 and "flags" in msg
+        rc, msg = _lib.bwd_check(args)
+        assert rc == -1 and "flags" in msg, f
     args.flags, args.dtype = _lib.BWD_ONLY_DQ, _lib.DTYPE_FP32
     rc, msg = _lib.bwd_check(args)
     assert rc == -2 and "fp32" in msg
-    args.flags, args.dtype = 0, _lib.DTYPE_BF16
+    args.flags = _lib.BWD_STORED_DS
+    assert _lib.bwd_check(args)[0] == 0
+    args.flags, args.dtype, args.workspace_bytes = 0, _lib.DTYPE_BF16, 0
 
 
 def test_abi_backward_noalloc_limit(built_library):
@@ -233,9 +239,14 @@ def test_abi_backward_noalloc_limit(built_library):
 
 
 def test_abi_backward_workspace(built_library):
-    """Workspace size: (L*log2e, delta) fp32 pairs for every (b, h, query) with
-    queries padded to 128, 256-byte aligned. Too small or misaligned
-    workspaces are rejected before any launch."""
+    """Workspace size. Default path (and fp32, and LSFA_BWD_STORED_DS at
+    head_dim <= 64): (L*log2e, delta) fp32 pairs for every (b, h, query) with
+    queries padded to 128, 256-byte aligned. Stored-dS path
+    (LSFA_BWD_STORED_DS, bf16/fp16, head_dim above 64): those pairs, then dS
+    of a chunk of heads (seqlen_k rounded up to 32 by seqlen_q rounded up to
+    256 elements per head, as many heads as fit in 4 GiB, at least one). Too
+    small or misaligned workspaces are rejected before any launch; stored-dS
+    problems that run in several chunks take no LSFA_BWD_ONLY_* flag."""
     st = _lib._i64x4(2048, 512, 64, 1)
     args = _lib.BwdArgs(q=16, k=32, v=48, o=64, dout=80, lse=96, dq=112, dk=128, dv=144, workspace=4096,
                         workspace_bytes=0,
@@ -261,9 +272,44 @@ def test_abi_backward_workspace(built_library):
     rc, msg = _lib.bwd_check(args)
     assert rc == -1 and "aligned" in msg
     args.workspace = 4096
-    # fp32 needs only the (L, delta) pairs
+    # fp32 needs only the (L, delta) pairs, whatever the flags
     args.dtype = _lib.DTYPE_FP32
     assert _lib.bwd_workspace_size(args) == rows * 8
+    args.flags = _lib.BWD_STORED_DS
+    assert _lib.bwd_workspace_size(args) == rows * 8
+
+    # head_dim 64: the stored-dS flag does not apply
+    args.dtype = _lib.DTYPE_BF16
+    assert _lib.bwd_workspace_size(args) == rows * 8
+    # stored-dS path
+    args.head_dim = 128
+    args.flags = 0
+    assert _lib.bwd_workspace_size(args) == rows * 8
+    args.flags = _lib.BWD_STORED_DS
+    for nq, nk in ((8, 8), (256, 8), (257, 100), (1000, 3)):
+        args.seqlen_q, args.seqlen_k = nq, nk
+        ld = 4 * ((nq + 127) // 128 * 128) * 8
+        ds = 4 * ((nk + 31) // 32 * 32) * ((nq + 255) // 256 * 256) * 2
+        want = ld + (ds + 255) // 256 * 256
+        assert _lib.bwd_workspace_size(args) == want, (nq, nk)
+        args.workspace_bytes = want - 1
+        assert _lib.bwd_check(args)[0] == -1
+        args.workspace_bytes = want
+        assert _lib.bwd_check(args)[0] == 0
+    args.seqlen_k = 0  # no keys: no dS
+    assert _lib.bwd_workspace_size(args) == 4 * 1024 * 8
+    # several chunks: 4 x 32 heads of 16416 x 16640 elements (546 MB) run 7 heads at a time
+    args.batch, args.heads_q, args.heads_kv, args.seqlen_q, args.seqlen_k = 4, 32, 32, 16385, 16385
+    head = 16416 * 16640 * 2
+    ld = 128 * 16512 * 8
+    assert _lib.bwd_workspace_size(args) == ld + (7 * head + 255) // 256 * 256
+    args.workspace_bytes = 1 << 40
+    assert _lib.bwd_check(args)[0] == 0
+    args.flags = _lib.BWD_ONLY_DQ | _lib.BWD_STORED_DS
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -2 and "chunk" in msg
+    args.flags = _lib.BWD_ONLY_DQ
+    assert _lib.bwd_check(args)[0] == 0
 
 
 def _rope_args(**kw):

@@ -111,9 +111,11 @@ def test_config_backward_full_size(gpu, cfg):
             assert_grad_parity(got, ex, ra, f"config {cfg} (b={b},h={h}) {name}")
 
 
-def _abi_fwd_bwd(q, k, v, do, causal, scale, phases=(0,)):
-    """Forward with L, then backward, through the C ABI directly (the Python
-    mirror keeps the reference's square-only contract)."""
+def _abi_fwd_bwd(q, k, v, do, causal, scale, phases=(0,), poison=False):
+    """Forward with L, then backward (lsfa_bwd once per entry of phases, with
+    that entry as flags), through the C ABI directly (the Python mirror keeps
+    the reference's square-only contract). poison: the workspace starts as
+    NaN bytes."""
     from lightserve_amd import _lib
     B, H, Nq, D = q.shape
     Nk = k.shape[2]
@@ -135,9 +137,11 @@ def _abi_fwd_bwd(q, k, v, do, causal, scale, phases=(0,)):
                       dq_stride=_lib.strides4(dq), dk_stride=_lib.strides4(dk), dv_stride=_lib.strides4(dv),
                       lse_stride=_lib._i64x3(*L.stride()), cu_seqlens_q=None, cu_seqlens_k=None, dtype=dt,
                       batch=B, heads_q=H, heads_kv=H, seqlen_q=Nq, seqlen_k=Nk, head_dim=D,
-                      causal=int(causal), sm_scale=scale, flags=0)
+                      causal=int(causal), sm_scale=scale, flags=phases[0])
     n = _lib.bwd_workspace_size(ba)
     ws = torch.empty(max(n, 1), device=q.device, dtype=torch.uint8)
+    if poison:
+        ws.fill_(0xFF)
     ba.workspace, ba.workspace_bytes = ws.data_ptr(), n
     for f in phases:
         ba.flags = f
@@ -145,16 +149,17 @@ def _abi_fwd_bwd(q, k, v, do, causal, scale, phases=(0,)):
     return o, L, dq, dk, dv
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("Nq,Nk", [(70, 200), (200, 70), (1, 129), (129, 1)])
-def test_abi_backward_non_square(gpu, Nq, Nk, causal, dtype):
+@pytest.mark.parametrize("Nq,Nk", [(70, 200), (200, 70), (1, 129), (129, 1), (300, 555), (555, 300)])
+def test_abi_backward_non_square(gpu, Nq, Nk, causal, dtype, D):
     """Nq != Nk through the C ABI: causal masking is bottom-right aligned
     (query i sees keys <= i + Nk - Nq); rows that see no key get zero
     gradients and L = -inf."""
-    print(f"case abi bwd Nq={Nq} Nk={Nk} causal={causal} {dtype}", flush=True)
+    print(f"case abi bwd Nq={Nq} Nk={Nk} causal={causal} {dtype} D={D}", flush=True)
     g = torch.Generator().manual_seed(5)
-    B, H, D = 2, 3, 64
+    B, H = 2, 3
     q, do = (torch.randn(B, H, Nq, D, generator=g).to(dtype).to(gpu) for _ in range(2))
     k, v = (torch.randn(B, H, Nk, D, generator=g).to(dtype).to(gpu) for _ in range(2))
     scale = D ** -0.5
@@ -174,17 +179,50 @@ def test_abi_backward_non_square(gpu, Nq, Nk, causal, dtype):
                                    msg=lambda m: f"{name}: {m}")
 
 
+@pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("causal", [False, True])
-def test_abi_backward_phases(gpu, causal):
-    """lsfa_bwd with LSFA_BWD_ONLY_DQ, then LSFA_BWD_ONLY_DKDV on the same
-    workspace (the timing mode the benchmark uses) gives the full call's
-    gradients bit for bit."""
+def test_abi_backward_phases(gpu, causal, stored):
+    """The backward's phases one at a time on one workspace (the timing mode
+    the benchmark uses) give the full call's gradients bit for bit: default
+    path LSFA_BWD_ONLY_DQ (which writes the per-row values) then
+    LSFA_BWD_ONLY_DKDV; stored-dS path LSFA_BWD_ONLY_DKDV (which stores dS)
+    then LSFA_BWD_ONLY_DQ. The workspace starts as NaN bytes in both runs, so
+    a phase that reads what it did not write fails."""
     from lightserve_amd import _lib
-    print(f"case abi bwd phases causal={causal}", flush=True)
+    print(f"case abi bwd phases causal={causal} stored={stored}", flush=True)
     g = torch.Generator().manual_seed(6)
     q, k, v, do = (torch.randn(2, 3, 300, 128, generator=g).to(torch.bfloat16).to(gpu) for _ in range(4))
-    full = _abi_fwd_bwd(q, k, v, do, causal, 128 ** -0.5)
-    split = _abi_fwd_bwd(q, k, v, do, causal, 128 ** -0.5, phases=(_lib.BWD_ONLY_DQ, _lib.BWD_ONLY_DKDV))
+    r = _lib.BWD_STORED_DS if stored else 0
+    order = (_lib.BWD_ONLY_DKDV, _lib.BWD_ONLY_DQ) if stored else (_lib.BWD_ONLY_DQ, _lib.BWD_ONLY_DKDV)
+    full = _abi_fwd_bwd(q, k, v, do, causal, 128 ** -0.5, phases=(r,), poison=True)
+    split = _abi_fwd_bwd(q, k, v, do, causal, 128 ** -0.5, phases=tuple(f | r for f in order), poison=True)
     torch.cuda.synchronize()
     for a, b in zip(full, split):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B,H,Nq,Nk,causal", [(2, 3, 300, 300, True), (1, 2, 700, 333, True), (1, 2, 333, 700, True),
+                                               (2, 2, 513, 513, False), (1, 9, 16384, 16384, False)])
+def test_stored_ds_matches_default(gpu, B, H, Nq, Nk, causal):
+    """The stored-dS path (LSFA_BWD_STORED_DS, head dim 128) against the
+    default path on the same inputs: dV comes from the same kernel arithmetic
+    and is equal bit for bit; dK (delta summed in another order) and dQ (a
+    GEMM over the stored dS instead of recomputed S and dP) agree to bf16
+    rounding. Non-square causal shapes leave dS blocks left of a key block's
+    first query tile unwritten (NaN here), which the dQ GEMM must mask. 9
+    heads of 16384 x 16384 need 4.5 GiB of dS, more than one 4 GiB chunk, so
+    that case runs the dK/dV kernel and the dQ GEMM in two chunks of heads."""
+    from lightserve_amd import _lib
+    print(f"case stored-dS vs default {B}x{H} Nq={Nq} Nk={Nk} causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(7)
+    q, do = (torch.randn(B, H, Nq, 128, generator=g).to(torch.bfloat16).to(gpu) for _ in range(2))
+    k, v = (torch.randn(B, H, Nk, 128, generator=g).to(torch.bfloat16).to(gpu) for _ in range(2))
+    _, _, dq0, dk0, dv0 = _abi_fwd_bwd(q, k, v, do, causal, 128 ** -0.5, phases=(_lib.BWD_STORED_DS,), poison=True)
+    _, _, dq1, dk1, dv1 = _abi_fwd_bwd(q, k, v, do, causal, 128 ** -0.5, poison=True)
+    torch.cuda.synchronize()
+    assert torch.equal(dv0, dv1)
+    for name, a, b in (("dq", dq0, dq1), ("dk", dk0, dk1)):
+        assert torch.isfinite(a).all(), name
+        err = (a.float() - b.float()).abs()
+        scale = b.float().abs().max().item()
+        assert err.max().item() <= 1e-2 * scale and err.mean().item() <= 1e-3 * scale, (name, err.max().item(), scale)

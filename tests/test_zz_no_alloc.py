@@ -2,10 +2,10 @@
 lsfa_bwd on the same arguments.
 
 lsfa_bwd_noalloc takes lsfa_bwd's arguments but ignores the workspace: it
-runs the same kernels with the library's own device scratch array, so its
-gradients must equal lsfa_bwd's bit for bit. Two calls in a row, the second
-with a smaller problem (the array keeps the first call's contents), and the
-split-phase timing mode through the same array.
+runs lsfa_bwd's default kernels with the library's own device scratch array,
+so its gradients must equal lsfa_bwd's bit for bit. Two calls in a row, the
+second with a smaller problem (the array keeps the first call's contents),
+and the split-phase timing mode through the same array.
 """
 import pytest
 import torch
