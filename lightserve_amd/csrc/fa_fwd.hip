@@ -7,10 +7,15 @@
 // the running row max is raised, p = exp(s - m) and alpha = exp(m_old - m),
 // l = alpha*l + sum(p), acc = alpha*acc + p(cast to the input dtype) @ V; at
 // the end o = acc / l and lse = m + ln(l). One difference in bookkeeping, not
-// in the result: the running max used as the exponent offset is only raised
-// when a row's tile max exceeds it by more than 2^8 (so p <= 256 and the
-// rescale of acc is skipped on most tiles); m + log(l) is unchanged by the
-// choice of offset.
+// in the result: the exponent offset m is the first tile's row max and is
+// only raised where p would come near the input dtype's range (above 2^64 for
+// bf16, whose exponent range is fp32's, or 2^15 for fp16), so most tiles need
+// neither a row max nor a rescale of acc; m + log(l) is unchanged by the
+// choice of offset. A tile's exponentials are computed with the current
+// offset and their row sums checked before the PV products use them: a sum
+// above the limit (rare: scores above the first tile's max by more than 44 /
+// 10 natural-log units) sends the tile through the row max, the rescale and
+// its exponentials again.
 //
 // Work decomposition
 //   workgroup = 4 waves = 128 query rows of one (batch, head); wave w owns
@@ -37,7 +42,10 @@
 namespace lsfa {
 
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kRescaleThreshold = 8.0f;  // log2 units
+// Largest log2 of p the PV operands may carry: a row's offset is raised once
+// its scores (in log2 units) exceed it by more than this.
+template <typename T> constexpr float kMaxLog2P = 64.0f;
+template <> constexpr float kMaxLog2P<_Float16> = 15.0f;
 
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool LSE, bool PAGED>
 __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
@@ -174,9 +182,11 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
-  // l_run: sum of the rounded p (normalises O); l_lse: sum of the fp32 p
+  // l_run: sum of the rounded p the PV products take (normalises O, so the
+  // weights of the V rows sum to one exactly); l_lse: sum of the fp32 p
   // (kept only for the logsumexp output, as the reference's l_i).
   float m_run = -1e30f, l_run = 0.f, l_lse = 0.f;
+  const float kTileSumMax = __builtin_exp2f(kMaxLog2P<T>);
 
   // K tile t lives in buffer t&1 (smem + (t&1)*TILE), V tile t in 2 + (t&1).
   auto kbuf = [&](int t) { return sbytes + (t & 1) * TILE * 2; };
@@ -205,42 +215,55 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
     mx = half_max(mx);
     return mx == -INFINITY ? -INFINITY : mx * sl2;
   };
-  // Raise the running offset only where a row max moved by more than the
-  // threshold (wave-uniform branch, taken on few tiles): O and l rescale in
-  // place.
-  auto raise_offset = [&](float mxs) {
-    if (__builtin_amdgcn_ballot_w64(mxs > m_run + kRescaleThreshold) != 0) {
-      const float m_new = fmaxf(m_run, mxs);
-      const float alpha = fast_exp2(m_run - m_new);
-      l_run *= alpha;
-      if constexpr (LSE) l_lse *= alpha;
-      m_run = m_new;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-    }
-  };
-  // Exponentials, rounding to the input dtype and row sums. The row sum adds
-  // the rounded p that the MFMA multiplies (v_dot2 with ones), so numerator
-  // and denominator share the rounding of the dominant terms whatever the
-  // exponent offset.
-  auto softmax = [&](f32x16* s, X8* pb) {
+  // Exponentials with the current offset, rounded to the input dtype into
+  // the PV operands; returns this lane's part of the tile's row sums: x = the
+  // rounded p (v_dot2 with ones), y = the fp32 p with LSE (four interleaved
+  // partial sums), else 0. s is left as it is.
+  auto softmax = [&](const f32x16* s, X8* pb) -> float2 {
     const float neg_m = -m_run;
-    float rs[4] = {0.f, 0.f, 0.f, 0.f};
-    float re = 0.f;
+    float rs[4] = {0.f, 0.f, 0.f, 0.f}, re[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
+      f32x16 p;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        s[kb][i] = fast_exp2(fmaf(s[kb][i], sl2, neg_m));
-        if constexpr (LSE) re += s[kb][i];
+        p[i] = fast_exp2(fmaf(s[kb][i], sl2, neg_m));
+        if constexpr (LSE) re[i & 3] += p[i];
       }
-      pb[2 * kb] = pack8<T>(s[kb], 0);
-      pb[2 * kb + 1] = pack8<T>(s[kb], 8);
+      pb[2 * kb] = pack8<T>(p, 0);
+      pb[2 * kb + 1] = pack8<T>(p, 8);
       sum8_into(pb[2 * kb], rs);
       sum8_into(pb[2 * kb + 1], rs);
     }
-    l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
-    if constexpr (LSE) l_lse += re;
+    float2 r;
+    r.x = (rs[0] + rs[1]) + (rs[2] + rs[3]);
+    r.y = LSE ? (re[0] + re[1]) + (re[2] + re[3]) : 0.f;
+    return r;
+  };
+  auto add_sums = [&](float2 ts) {
+    l_run += ts.x;
+    if constexpr (LSE) l_lse += ts.y;
+  };
+  // The exponentials of a tile, checked: if some row's sum passes the limit
+  // (a p above 2^kMaxLog2P, or inf; wave-uniform branch, taken on few tiles),
+  // that row's offset rises to its max in this tile, O and l rescale in
+  // place, and the exponentials are computed again.
+  auto softmax_checked = [&](const f32x16* s, X8* pb) {
+    float2 ts = softmax(s, pb);
+    if (__builtin_amdgcn_ballot_w64(ts.x > kTileSumMax) != 0) {
+      const float mx = row_max(s);
+      if (__builtin_amdgcn_ballot_w64(mx > m_run) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = fast_exp2(m_run - m_new);
+        l_run *= alpha;
+        if constexpr (LSE) l_lse *= alpha;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+      }
+      ts = softmax(s, pb);
+    }
+    add_sums(ts);
   };
   // O^T += V^T P^T with V^T from transpose reads.
   auto pv = [&](const LDS_AS char* Vs, const X8* pb) {
@@ -256,42 +279,65 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
     }
   };
 
-  // Tiles [0, n_full) are fully visible to every row of the workgroup (inside
-  // the sequence and, when causal, at or below the diagonal of its first row).
-  // They run software-pipelined: while the MFMAs of S for tile j+1 issue, the
-  // VALU computes tile j's exponentials; while tile j's PV MFMAs issue, it
-  // computes tile j+1's row max. Tiles [n_full, ntiles) then run one at a
-  // time with masking. Buffers: K tile t+2 and V tile t+1 load while tile t
-  // is processed (K runs one tile ahead of V).
-  int n_full = min(ntiles, nk / BN);
-  if (CAUSAL) n_full = min(n_full, max(0, q0 + off + 1) / BN);
+  // Every key tile runs software-pipelined: while the MFMAs of S for tile t+1
+  // issue, the VALU computes tile t's exponentials (with the first tile's
+  // offset and the overflow check), then tile t's PV MFMAs issue. A wave
+  // skips the tiles it cannot see (causal: keys past its last row's
+  // diagonal) and, before their exponentials, masks to -inf the scores of
+  // the tiles it sees in part (the diagonal, the sequence end), so that
+  // their p are exactly 0. Buffers: K tile t+2 and V tile t+1 load while
+  // tile t is processed (K runs one tile ahead of V).
+  auto wave_sees = [&](int j) { return !CAUSAL || j * BN <= qw_lo + 31 + off; };
+  auto mask_tile = [&](int j, f32x16* s) {
+    const int kbase = j * BN;
+    if ((kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > qw_lo + off)) {
+      // (the empty volatile asm keeps this a branch: the selects below would
+      // otherwise be hoisted out of it and run on every tile)
+      asm volatile("" ::: "memory");
+      int lim = nk - 1 - kbase - 4 * hh;
+      if (CAUSAL) lim = min(lim, qrow + off - kbase - 4 * hh);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          s[kb][i] = 32 * kb + 8 * (i >> 2) + (i & 3) > lim ? -INFINITY : s[kb][i];
+    }
+  };
 
   // blk1, blk2: blocks of tiles t+1 and t+2 for the next pipelined step t.
   const int blk0 = block_of(0);
   int blk1 = block_of(1), blk2 = block_of(2);
-  tile_load(K, p.skn, p.skb, p.skh, kvo, 0, 0, blk0);
-  tile_load(V, p.svn, p.svb, p.svh, vvo, 0, 2, blk0);
-  tile_load(K, p.skn, p.skb, p.skh, kvo, 1, 1, blk1);  // past the end the descriptor is empty: zeros
+  if (ntiles > 0) {
+    tile_load(K, p.skn, p.skb, p.skh, kvo, 0, 0, blk0);
+    tile_load(V, p.svn, p.svb, p.svh, vvo, 0, 2, blk0);
+  }
+  if (ntiles > 1) tile_load(K, p.skn, p.skb, p.skh, kvo, 1, 1, blk1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
+  // The offset starts at the first tile's row max (rows that see none of its
+  // keys keep -1e30: their first visible tile then takes the check's slow
+  // path, which raises the offset to that tile's max).
   f32x16 s0[KB], s1[KB];
-  if (n_full > 0) {
+  if (ntiles > 0 && wave_sees(0)) {
     scores(kbuf(0), s0);
-    m_run = row_max(s0);  // every row sees the whole tile: finite
-    __syncthreads();      // K buffer 0 is refilled by the first step
+    mask_tile(0, s0);
+    m_run = fmaxf(row_max(s0), -1e30f);
   }
-  // One pipelined step: tile t's scores are in cur (offset already raised),
-  // tile t+1's go to nxt.
+  __syncthreads();  // K buffer 0 is refilled by the first step
+  // One pipelined step: tile t's scores are in cur, tile t+1's go to nxt.
   auto pipe_step = [&](int t, f32x16* cur, f32x16* nxt) {
-    tile_load(K, p.skn, p.skb, p.skh, kvo, t + 2, t & 1, blk2);
-    tile_load(V, p.svn, p.svb, p.svh, vvo, t + 1, 2 + ((t + 1) & 1), blk1);
-    scores(kbuf(t + 1), nxt);
-    X8 pb[2 * KB];
-    softmax(cur, pb);
-    pv(vbuf(t), pb);
-    const float mxs = row_max(nxt);
-    if (t + 1 < n_full) raise_offset(mxs);
+    if (t + 2 < ntiles) tile_load(K, p.skn, p.skb, p.skh, kvo, t + 2, t & 1, blk2);
+    if (t + 1 < ntiles) tile_load(V, p.svn, p.svb, p.svh, vvo, t + 1, 2 + ((t + 1) & 1), blk1);
+    if (t + 1 < ntiles && wave_sees(t + 1)) {
+      scores(kbuf(t + 1), nxt);
+      mask_tile(t + 1, nxt);
+    }
+    if (wave_sees(t)) {
+      X8 pb[2 * KB];
+      softmax_checked(cur, pb);
+      pv(vbuf(t), pb);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (PAGED) {
       // The next step's block id is read after this step's last LDS read:
@@ -303,43 +349,11 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
     __syncthreads();
   };
   int j = 0;
-  for (; j + 1 < n_full; j += 2) {
+  for (; j + 1 < ntiles; j += 2) {
     pipe_step(j, s0, s1);
     pipe_step(j + 1, s1, s0);
   }
-  if (j < n_full) {
-    pipe_step(j, s0, s1);
-    ++j;
-  }
-
-  // Remaining tiles (diagonal / sequence end), masked, one at a time. K of
-  // tile n_full + 1 is already in flight from the pipelined part.
-  for (; j < ntiles; ++j) {
-    const int bj = block_of(j + 1);
-    if (j > n_full) tile_load(K, p.skn, p.skb, p.skh, kvo, j + 1, (j + 1) & 1, bj);
-    tile_load(V, p.svn, p.svb, p.svh, vvo, j + 1, 2 + ((j + 1) & 1), bj);
-    const int kbase = j * BN;
-    const bool active = !CAUSAL || (kbase <= qw_lo + 31 + off);
-    if (active) {
-      scores(kbuf(j), s0);
-      const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > qw_lo + off);
-      if (need_mask) {
-        int lim = nk - 1 - kbase - 4 * hh;
-        if (CAUSAL) lim = min(lim, qrow + off - kbase - 4 * hh);
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (32 * kb + 8 * (i >> 2) + (i & 3) > lim) s0[kb][i] = -INFINITY;
-      }
-      raise_offset(row_max(s0));
-      X8 pb[2 * KB];
-      softmax(s0, pb);
-      pv(vbuf(j), pb);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  }
+  if (j < ntiles) pipe_step(j, s0, s1);
 
   const float lt = half_sum(l_run);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
