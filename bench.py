@@ -909,6 +909,7 @@ def main():
                          "dq_gemm_bytes": dq_bytes}
             stored_ds["dq_gemm_gbs"] = round(dq_bytes / (stored_ds["dq_gemm_ms"] * 1e-3) / 1e9, 1)
             stored_ds["dq_gemm_hbm_frac"] = round(stored_ds["dq_gemm_gbs"] / HBM_PEAK_GBS, 4)
+            stored_ds["dq_gemm_traffic"] = measured_traffic("fa_bwd_dq_ds_kernel", wl_key)
             del keep
     for kd in kernels:
         kd["achieved"] = round(kd["flops_per_launch"] / (kd["avg_launch_ms"] * 1e-3) / 1e12, 2)

@@ -60,6 +60,35 @@ def test_matches_oracle_reference_shapes(gpu, B, H, N, D, dtype, causal):
     assert torch.equal(o_only, o), "return_lse must not change the output"
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_offset_raised_by_later_tiles(gpu, D, dtype, causal):
+    """The forward's exponent offset starts at the first key tile's row max
+    and is raised only when a tile's exponentials come near the operand
+    dtype's range (2^64 for bf16, 2^15 for fp16). Here a few keys far into the
+    sequence score ~55 natural-log units above everything in the first tile
+    (q has a common component, the spike keys are constant vectors along
+    it), which must take the raise-and-recompute path on that tile; the
+    spike keys then carry nearly all of the weight of the rows that see
+    them."""
+    print(f"case fwd offset raise D={D} {dtype} causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    B, H, N = 1, 2, 600
+    q = torch.randn(B, H, N, D, generator=g) * 0.3 + 1.0
+    k = torch.randn(B, H, N, D, generator=g) * 0.5
+    v = torch.randn(B, H, N, D, generator=g)
+    spikes = [301, 302, 450, 451, 452]
+    k[:, :, spikes, :] = 55.0 / math.sqrt(D)
+    q, k, v = (t.to(dtype).to(gpu) for t in (q, k, v))
+    o, lse = flash_attention_forward(q, k, v, causal=causal, return_lse=True)
+    o_ref, lse_ref = _oracle_cpu(q, k, v, causal)
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
+    assert_gate(o.cpu(), o_ref, f"o {dtype}")
+    assert_lse(lse.cpu(), lse_ref, "lse")
+    assert lse_ref.max() > 40  # the spikes dominate the rows that see them
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_matches_oracle_non_contiguous(gpu, dtype):
     """The reference's transposed-heads view (kernels/tests/test_flash_attention.py:65-77)."""
