@@ -278,6 +278,18 @@ __global__ __launch_bounds__(256) void fa_gemv_kernel(const GemvParams p) {
         __hip_atomic_store(p.partial + ((int64_t)split * p.M + m) * p.N + n, sum[m], __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
   }
+  // Handoff to the workgroup that arrives last, built on gfx950's device
+  // coherence rather than on release/acquire fences: the partials are
+  // agent-scope atomic stores (write-through to the device-coherent level,
+  // sc1), every wave waits for their completion (vmcnt(0)) before the
+  // barrier and thread 0's agent-scope counter RMWs, and the last workgroup
+  // reads them with agent-scope atomic loads (sc1: never a stale line of its
+  // own XCD's L2) issued only after its RMW has returned. Release/acquire
+  // fences at agent scope would be the HIP memory model's way; they lower to
+  // a whole-L2 write-back (buffer_wbl2 sc1) per arrival and an invalidate
+  // (buffer_inv sc1) per acquire, and measured 1.4-1.9x slower on the
+  // LM-head product (6.7 -> 3.6-4.8 TB/s), more on the narrow decode
+  // projections whose ~1000 workgroups each would pay a write-back.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partials have reached device scope
   __syncthreads();
   if (tid == 0) {

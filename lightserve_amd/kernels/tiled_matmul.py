@@ -37,11 +37,15 @@ LSFA_GEMV_COUNTER_BYTES) that must start at zero and that every call leaves
 at zero, so this module keeps one workspace per (device, stream), zeroes its
 counter bytes once when it is created, and reuses it for every call on that
 stream (stream order keeps the calls apart). Workspaces start at 16 MB, so
-they rarely grow; one that grows is replaced, not freed: a captured HIP graph
-that recorded the old one keeps using it. (A workspace first created inside
-a graph capture records its counter fill into the graph, which then clears
-the 256 KB on every replay.)
+they rarely grow. The cache is bounded: a workspace that grows is freed
+unless a graph capture used it (a captured HIP graph that recorded it keeps
+using it, so such workspaces stay until release_workspaces()), and at most
+MAX_CACHED_STREAMS streams keep one, the least recently used uncaptured entry
+going first. (A workspace first created inside a graph capture records its
+counter fill into the graph, which then clears the 256 KB on every replay.)
 """
+import collections
+
 import torch
 
 from .. import _lib
@@ -55,16 +59,47 @@ AUTO_MAX_ROWS = 2    # rows that every product (and the fused norm / SwiGLU inpu
 MFMA_AUTO_ROWS = 8
 MFMA_AUTO_MAX_COLS = 8192
 
-_workspaces = {}  # (device index, stream handle) -> every workspace created for it, the last in use
+MAX_CACHED_STREAMS = 8
+
+
+class _Entry:
+    __slots__ = ("buf", "captured", "kept")
+
+    def __init__(self):
+        self.buf = None       # the workspace in use
+        self.captured = False  # a graph capture used buf
+        self.kept = []         # smaller workspaces a captured graph may still use
+
+
+# (device index, stream handle) -> _Entry, least recently used first
+_workspaces = collections.OrderedDict()
 
 
 def _workspace(device, stream, nbytes):
-    bufs = _workspaces.setdefault((device.index, stream), [])
-    if not bufs or bufs[-1].numel() < nbytes:
-        buf = torch.empty(max(nbytes, 16 << 20), dtype=torch.uint8, device=device)
-        buf[:_lib.GEMV_COUNTER_BYTES].zero_()
-        bufs.append(buf)
-    return bufs[-1]
+    key = (device.index, stream)
+    entry = _workspaces.pop(key, None) or _Entry()
+    if entry.buf is None or entry.buf.numel() < nbytes:
+        if entry.buf is not None and entry.captured:
+            entry.kept.append(entry.buf)
+        entry.buf = torch.empty(max(nbytes, 16 << 20), dtype=torch.uint8, device=device)
+        entry.buf[:_lib.GEMV_COUNTER_BYTES].zero_()
+        entry.captured = False
+    if torch.cuda.is_current_stream_capturing():
+        entry.captured = True
+    _workspaces[key] = entry
+    while len(_workspaces) > MAX_CACHED_STREAMS:
+        victim = next((k for k, e in _workspaces.items() if not e.captured and not e.kept), None)
+        if victim is None:
+            break
+        del _workspaces[victim]
+    return entry.buf
+
+
+def release_workspaces():
+    """Frees every cached skinny-GEMM workspace. Call it once no captured HIP
+    graph that ran a skinny product is alive (those graphs keep using the
+    workspaces they recorded)."""
+    _workspaces.clear()
 
 
 def _skinny_ok(a: torch.Tensor, b: torch.Tensor, max_rows: int = SKINNY_MAX_ROWS) -> bool:

@@ -162,6 +162,52 @@ def test_skinny_matmul_in_graph_replays():
         assert torch.equal(y, eager), f"replay {i}"
 
 
+def test_skinny_workspace_cache_is_bounded():
+    """The skinny GEMM's per-stream workspace cache keeps at most
+    MAX_CACHED_STREAMS entries (the least recently used entry no graph capture
+    used goes first), results stay exact on every stream, a workspace used
+    under graph capture is kept, and release_workspaces() empties the cache."""
+    from lightserve_amd.kernels import tiled_matmul as tm
+    print("case skinny workspace cache", flush=True)
+    tm.release_workspaces()
+    torch.manual_seed(9)
+    a = torch.randn(1, 8192, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(8192, 1024, device="cuda", dtype=torch.bfloat16)
+    args = _lib.GemvArgs(x=16, w=16, y=16, workspace=None, workspace_bytes=0, x_stride=8192, w_stride=1024,
+                         y_stride=1024, dtype=_lib.DTYPE_BF16, m=1, k=8192, n=1024)
+    assert _lib.gemv_workspace_size(args) > 0  # split K: the call needs a workspace
+    ref = tm.skinny_matmul(a, b)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(tm.MAX_CACHED_STREAMS + 4)]
+    for s in streams:
+        with torch.cuda.stream(s):
+            out = tm.skinny_matmul(a, b)
+        s.synchronize()
+        assert torch.equal(out, ref)
+        assert len(tm._workspaces) <= tm.MAX_CACHED_STREAMS
+    # a capture on a fresh stream marks its workspace as used by a graph
+    cap = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        out = tm.skinny_matmul(a, b)  # creates the workspace (and zeroes its counters) outside the capture
+        cap.synchronize()
+        with torch.cuda.graph(g, stream=cap):
+            out = tm.skinny_matmul(a, b)
+    key = (torch.cuda.current_device(), cap.cuda_stream)
+    assert tm._workspaces[key].captured
+    for s in streams:
+        with torch.cuda.stream(s):
+            tm.skinny_matmul(a, b)
+        s.synchronize()
+    assert key in tm._workspaces  # captured: never evicted
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    del g
+    tm.release_workspaces()
+    assert not tm._workspaces
+
+
 def test_skinny_matmul_counters_return_to_zero():
     """The last workgroup of each column block clears its arrival counter:
     after calls of several shapes the stream's workspace counters read zero,
@@ -176,7 +222,7 @@ def test_skinny_matmul_counters_return_to_zero():
         again = tiled_matmul.skinny_matmul(x, w)
         torch.cuda.synchronize()
         assert torch.equal(first, again), (M, K, N)
-        ws = tiled_matmul._workspaces[(0, torch.cuda.current_stream().cuda_stream)][-1]
+        ws = tiled_matmul._workspaces[(0, torch.cuda.current_stream().cuda_stream)].buf
         # the whole counter region: the VALU kernel keeps 16 counters per 256
         # columns, the MFMA kernel (3 and 8 rows here) 16 per 128
         assert (ws[:_lib.GEMV_COUNTER_BYTES] == 0).all(), (M, K, N)
