@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
   int bh, qt;
-  map_tile(p.num_tiles, gridDim.x, bh, qt, CAUSAL);
+  map_tile(p.num_tiles, gridDim.x, p.heads_per_group, bh, qt, CAUSAL);
   const int b = bh / p.H, h = bh - b * p.H;
   const int nq = p.Nq, nk = p.Nk, D = p.D;
   const int q0 = qt * BM;
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   const int kb = wave;
   const bool w_hi = wave >= NW / 2;  // waves 2, 3 load dO; 0, 1 load Q
   int bh, kt;
-  map_tile(p.num_tiles, gridDim.x, bh, kt, false);  // low key tiles see the most queries
+  map_tile(p.num_tiles, gridDim.x, p.heads_per_group, bh, kt, false);  // low key tiles see the most queries
   bh += p.bh0;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nq = p.Nq, nk = p.Nk, D = p.D;
@@ -716,7 +716,7 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dq_ds_kernel(const BwdParams p)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hh = lane >> 5;
   int bh, qt;
-  map_tile(p.num_tiles, gridDim.x, bh, qt, CAUSAL);
+  map_tile(p.num_tiles, gridDim.x, p.heads_per_group, bh, qt, CAUSAL);
   bh += p.bh0;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nq = p.Nq, nk = p.Nk, D = p.D;
@@ -890,11 +890,13 @@ static hipError_t launch_bwd_ds(BwdParams p, int phases, hipStream_t s) {
     const int n = BH - bh0 < p.nbh ? BH - bh0 : p.nbh;
     if ((phases & 2) && ktiles > 0) {
       c.num_tiles = ktiles;
+      c.heads_per_group = heads_per_group_for((long long)p.Nq * 128 * 2 * 2);  // Q and dO rows of a head
       hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, 128, CAUSAL, true>), dim3(ktiles * n), dim3(256), 0, s, c);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if ((phases & 1) && qtiles > 0) {
       c.num_tiles = qtiles;
+      c.heads_per_group = heads_per_group_for((long long)p.Nk * 128 * 2);  // K rows of a head (dS streams once)
       hipLaunchKernelGGL((fa_bwd_dq_ds_kernel<T, 128, CAUSAL>), dim3(qtiles * n), dim3(512), 0, s, c);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
@@ -919,11 +921,13 @@ static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
   p.bh0 = 0;
   p.nbh = BH;
   p.num_tiles = (p.Nq + 127) / 128;
+  p.heads_per_group = heads_per_group_for((long long)p.Nk * DP * 2 * 2);  // K and V rows of a head
   if ((phases & 1) && p.num_tiles > 0) {
     hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   p.num_tiles = (p.Nk + 127) / 128;
+  p.heads_per_group = heads_per_group_for((long long)p.Nq * DP * 2 * 2);  // Q and dO rows of a head
   if ((phases & 2) && p.num_tiles > 0) {
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
     e = hipGetLastError();

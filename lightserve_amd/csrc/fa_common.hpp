@@ -159,6 +159,7 @@ struct FwdParams {
   int block_shift, max_blocks, num_blocks;
   int B, Hq, Hkv, Nq, Nk, D;
   int num_q_tiles;
+  int heads_per_group;  // map_tile grouping
   float scale_log2;  // |sm_scale| * log2(e), at least 1e-30
   int neg_q;         // sm_scale < 0: q is negated on load so scale_log2 stays positive
 };
@@ -196,6 +197,7 @@ struct BwdParams {
   int64_t sqd, skd, svd, sod, sdod, sdqd, sdkd, sdvd;  // fp32 path only
   int B, H, Nq, Nk, D;
   int num_tiles;     // tiles per (b, h) along the kernel's stationary axis
+  int heads_per_group;  // map_tile grouping
   float scale;       // sm_scale
   float scale_log2;  // sm_scale * log2(e)
 };
@@ -305,16 +307,34 @@ struct NormParams {
 
 // Maps the 1-D launch index to (batch*head, tile). Workgroups are handed to
 // the 8 XCDs round-robin by launch index, so consecutive launch indices are
-// spread so that each XCD owns a contiguous run of heads (their K/V stay in
-// that XCD's L2), and within a head the tiles are issued heaviest-first
-// (largest causal extent first) for load balance.
-__device__ __forceinline__ void map_tile(int num_tiles, int total, int& bh, int& tile, bool heavy_last_index) {
+// spread so that each XCD owns a contiguous run of heads (their operands stay
+// in that XCD's L2). Within a run, heads go in groups of heads_per_group and
+// each group's tiles are issued heaviest-first across the whole group (largest
+// causal extent first: all its heads' heaviest tiles, then the next level):
+// the late, light tiles of one group overlap the heavy ones of the next, so
+// the grid's tail is short, while a group's streamed operands (a few MB)
+// stay in L2.
+__device__ __forceinline__ void map_tile(int num_tiles, int total, int heads_per_group, int& bh, int& tile,
+                                         bool heavy_last_index) {
   const int L = blockIdx.x;
   int W = L;
   if ((total & 7) == 0) W = (L & 7) * (total >> 3) + (L >> 3);
-  bh = W / num_tiles;
-  const int t = W - bh * num_tiles;
-  tile = heavy_last_index ? (num_tiles - 1 - t) : t;
+  const int BH = total / num_tiles;
+  const int hg = max(heads_per_group, 1);
+  const int g0 = (W / (hg * num_tiles)) * hg;  // first head of W's group
+  const int gh = min(hg, BH - g0);             // heads in the group
+  const int rr = W - g0 * num_tiles;
+  const int level = rr / gh;
+  bh = g0 + (rr - level * gh);
+  tile = heavy_last_index ? (num_tiles - 1 - level) : level;
+}
+
+// Heads per map_tile group: as many as keep a group's streamed operands
+// (bytes_per_head each: K and V for the query-stationary kernels, Q and dO
+// for the key-stationary one) within ~8 MiB, i.e. two XCD L2s, at most 16.
+inline int heads_per_group_for(long long bytes_per_head) {
+  const long long g = bytes_per_head > 0 ? (8LL << 20) / bytes_per_head : 16;
+  return (int)(g < 1 ? 1 : (g > 16 ? 16 : g));
 }
 
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *(const u32x4*)p; }

@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
   int bh, qt;
-  map_tile(p.num_q_tiles, gridDim.x, bh, qt, CAUSAL);
+  map_tile(p.num_q_tiles, gridDim.x, p.heads_per_group, bh, qt, CAUSAL);
   const int b = bh / p.Hq, h = bh - b * p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
   int nq = p.Nq, nk = p.Nk;
@@ -411,6 +411,7 @@ static hipError_t dispatch_fwd_t(const FwdParams& p, int dp, bool causal, bool v
 // dp is the padded head dim (32, 64 or 128). Query tiles are 128 rows.
 hipError_t fwd_mfma(FwdParams p, bool is_bf16, int dp, bool causal, bool varlen, hipStream_t s) {
   p.num_q_tiles = (p.Nq + 127) / 128;
+  p.heads_per_group = heads_per_group_for((long long)p.Nk * dp * 2 * 2);  // K and V rows of a head
   if (is_bf16) return dispatch_fwd_t<__bf16>(p, dp, causal, varlen, s);
   return dispatch_fwd_t<_Float16>(p, dp, causal, varlen, s);
 }
@@ -433,6 +434,7 @@ static hipError_t dispatch_paged_t(const FwdParams& p, int dp, bool causal, hipS
 // longest query chunk, block_shift >= 4).
 hipError_t fwd_paged(FwdParams p, bool is_bf16, int dp, bool causal, hipStream_t s) {
   p.num_q_tiles = (p.Nq + 127) / 128;
+  p.heads_per_group = heads_per_group_for((long long)p.Nk * dp * 2 * 2);
   if (is_bf16) return dispatch_paged_t<__bf16>(p, dp, causal, s);
   return dispatch_paged_t<_Float16>(p, dp, causal, s);
 }
