@@ -89,6 +89,33 @@ def test_offset_raised_by_later_tiles(gpu, D, dtype, causal):
     assert lse_ref.max() > 40  # the spikes dominate the rows that see them
 
 
+@pytest.mark.parametrize("B,H,N,causal", [(1, 13, 1024, True), (3, 5, 2048, True), (1, 13, 1500, False)])
+def test_grouped_tile_order_covers_every_tile(gpu, B, H, N, causal):
+    """Workgroups take (head, query tile) in groups of heads sized to a few MB
+    of K/V (here 4-16 heads: 13 and 15 heads leave a partial last group, and
+    13 * 8 = 104 or 13 * 12 = 156 tiles are or are not a multiple of the 8
+    XCDs): every query row of every head must be computed exactly once, so
+    each (b, h) slice matches the oracle, forward and backward."""
+    from lightserve_amd.kernels.flash_attention_backward import _flash_attention_backward, _flash_attention_forward_lse
+    print(f"case grouped order {B}x{H}x{N} causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    q, k, v, do = (torch.randn(B, H, N, 128, generator=g).to(torch.bfloat16).to(gpu) for _ in range(4))
+    o, lse = _flash_attention_forward_lse(q, k, v, causal)
+    dq, dk, dv = _flash_attention_backward(do, q, k, v, o, lse, causal)
+    torch.cuda.synchronize()
+    from tests.test_fa_backward_gpu import _grads_gpu_fp32
+    for b in range(B):
+        for h in range(H):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            o_ref, l_ref = attention_reference(q[sl].float(), k[sl].float(), v[sl].float(), causal, dtype=torch.float32)
+            assert_gate(o[sl].float(), o_ref, f"o (b={b},h={h})")
+            assert_lse(lse[sl], l_ref, f"lse (b={b},h={h})")
+            ref = _grads_gpu_fp32(q[sl], k[sl], v[sl], do[sl], causal)
+            for name, got, want in zip(("dq", "dk", "dv"), (dq[sl], dk[sl], dv[sl]), ref):
+                err = (got.float() - want.float()).abs()
+                assert err.max().item() <= 5e-2 and err.mean().item() <= 2e-3, (name, b, h, err.max().item())
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_matches_oracle_non_contiguous(gpu, dtype):
     """The reference's transposed-heads view (kernels/tests/test_flash_attention.py:65-77)."""
