@@ -70,7 +70,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   const int l32 = lane & 31, hh = lane >> 5;
   int bh, qt;
   map_tile(p.num_q_tiles, gridDim.x, p.heads_per_group, bh, qt, CAUSAL);
-  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  // Varlen sequences differ in length, so the (sequence, head) index runs
+  // head-major: each XCD's contiguous run of indices then holds a few heads
+  // (with GQA, the query heads of one KV head) of every sequence, instead of
+  // all heads of one sequence, and the XCDs get equal work.
+  const int b = VARLEN ? bh % p.B : bh / p.Hq;
+  const int h = VARLEN ? bh / p.B : bh - b * p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
   int nq = p.Nq, nk = p.Nk;
   int64_t rq0 = 0, rk0 = 0;
