@@ -47,6 +47,74 @@ constexpr float kLn2 = 0.6931471805599453f;
 template <typename T> constexpr float kMaxLog2P = 64.0f;
 template <> constexpr float kMaxLog2P<_Float16> = 15.0f;
 
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Number of a sequence's query tiles (tq of them, 128 rows each) whose key
+// tile count (64 keys each) exceeds x; the tiles counted are always the last
+// ones, as causal work grows with the tile index. x = -1 counts every tile.
+template <bool CAUSAL>
+__device__ __forceinline__ int tiles_above(int x, int tq, int nk, int off) {
+  if (x < 0) return tq;
+  if (tq == 0 || nk <= 64 * x) return 0;  // the last tile sees all nk keys
+  if (!CAUSAL) return tq;
+  // tile t < tq-1 sees off + 128(t+1) keys: more than 64x iff t >= (64x-off)/128
+  const long long y = 64LL * x - off;
+  return y < 0 ? tq : 1 + max(0, tq - 1 - (int)(y >> 7));
+}
+
+// Longest-first order of a varlen launch's (sequence, query tile) items, so
+// that each XCD starts its longest workgroups first and the short ones fill
+// the tail: returns the item of the given rank (rank 0 has the most key
+// tiles; ties go by sequence, then tile), or b = -1 past the last item.
+// Lane i holds sequence i (B <= 64). The key tile count of the item at the
+// rank is found by binary search on the number of items above a count, then
+// the item among those of that count by a prefix sum over the sequences.
+// Wave-uniform result.
+template <bool CAUSAL, bool PAGED>
+__device__ __forceinline__ void varlen_item_at(const FwdParams& p, int rank, int lane, int& b_out, int& qt_out) {
+  int tq = 0, nk = 0, off = 0;
+  if (lane < p.B) {
+    const int nq = p.cu_q[lane + 1] - p.cu_q[lane];
+    nk = PAGED ? min(max(p.seq_lens_k[lane], 0), p.max_blocks << p.block_shift)
+               : p.cu_k[lane + 1] - p.cu_k[lane];
+    tq = nq > 0 ? (nq + 127) >> 7 : 0;
+    off = nk - nq;
+  }
+  b_out = -1;
+  qt_out = 0;
+  if (rank >= wave_sum_i(tq)) return;
+  int kmax = nk > 0 ? (nk + 63) >> 6 : 0;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, __shfl_xor(kmax, o));
+  int lo = 0, hi = __builtin_amdgcn_readfirstlane(kmax);  // no item exceeds hi
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (__builtin_amdgcn_readfirstlane(wave_sum_i(tiles_above<CAUSAL>(mid, tq, nk, off))) <= rank) hi = mid;
+    else lo = mid + 1;
+  }
+  // rank lies among the items of exactly lo key tiles: tiles
+  // [tq - above(lo-1), tq - above(lo)) of each sequence.
+  const int a_hi = tiles_above<CAUSAL>(lo - 1, tq, nk, off);
+  const int a_lo = tiles_above<CAUSAL>(lo, tq, nk, off);
+  const int c = a_hi - a_lo;
+  const int k = rank - __builtin_amdgcn_readfirstlane(wave_sum_i(a_lo));
+  int inc = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o);
+    if (lane >= o) inc += t;
+  }
+  const int pre = inc - c;
+  const unsigned long long hit = __ballot(c > 0 && k >= pre && k < pre + c);
+  const int src = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit));
+  b_out = src;
+  qt_out = __builtin_amdgcn_readfirstlane(__shfl(tq - a_hi + k - pre, src));
+}
+
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool LSE, bool PAGED>
 __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   using X8 = typename VecT<T>::x8;
@@ -68,14 +136,27 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
-  int bh, qt;
-  map_tile(p.num_q_tiles, gridDim.x, p.heads_per_group, bh, qt, CAUSAL);
-  // Varlen sequences differ in length, so the (sequence, head) index runs
-  // head-major: each XCD's contiguous run of indices then holds a few heads
-  // (with GQA, the query heads of one KV head) of every sequence, instead of
-  // all heads of one sequence, and the XCDs get equal work.
-  const int b = VARLEN ? bh % p.B : bh / p.Hq;
-  const int h = VARLEN ? bh / p.B : bh - b * p.Hq;
+  int b, h, qt;
+  if (VARLEN && p.B <= 64) {
+    // Varlen sequences differ in length: workgroup L takes the item of rank
+    // L / Hq in longest-first order, for head slot L % Hq. Workgroups go to
+    // the XCDs round-robin, so with Hq a multiple of 8 XCD x gets slots
+    // x, x+8, ..., mapped to the adjacent heads x*Hq/8 .. (with GQA, query
+    // heads that share K/V), every rank in order.
+    const int L = blockIdx.x;
+    const int rank = L / p.Hq, u = L - rank * p.Hq;
+    h = (p.Hq & 7) == 0 ? (u & 7) * (p.Hq >> 3) + (u >> 3) : u;
+    varlen_item_at<CAUSAL, PAGED>(p, rank, lane, b, qt);
+    if (b < 0) return;  // uniform, before any barrier
+  } else {
+    int bh;
+    map_tile(p.num_q_tiles, gridDim.x, p.heads_per_group, bh, qt, CAUSAL);
+    // Longer varlen batches: the (sequence, head) index runs head-major, so
+    // each XCD's contiguous run of indices holds a few heads of every
+    // sequence instead of all heads of one sequence.
+    b = VARLEN ? bh % p.B : bh / p.Hq;
+    h = VARLEN ? bh / p.B : bh - b * p.Hq;
+  }
   const int hk = h / (p.Hq / p.Hkv);
   int nq = p.Nq, nk = p.Nk;
   int64_t rq0 = 0, rk0 = 0;

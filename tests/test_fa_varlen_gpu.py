@@ -1,5 +1,7 @@
 """GPU parity of the packed varlen GQA forward (config 5: chunked prefill over
 a cached prefix) against oracle.attention.varlen_reference."""
+import math
+
 import pytest
 import torch
 
@@ -60,3 +62,55 @@ def test_varlen_config5_full_size(gpu):
         ob, lb = attention_reference(qb, kb, vb, True, dtype=torch.float32)
         assert_gate(o[cq[b]:cq[b + 1]].transpose(0, 1), ob, f"config 5 seq {b}")
         assert_lse(lse[:, cq[b]:cq[b + 1]], lb, f"config 5 seq {b}")
+
+
+def _varlen_poisoned(q, k, v, cu_q, cu_k, max_q, max_k, causal):
+    """The varlen forward through the C ABI into NaN-filled o and lse, so a
+    (sequence, head, query tile) that no workgroup takes shows as NaN."""
+    from lightserve_amd import _lib
+    from lightserve_amd.kernels.flash_attention import lse_args
+    Tq, Hq, D = q.shape
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full((Hq, Tq), float("nan"), device=q.device, dtype=torch.float32)
+    lse_ptr, _ = lse_args(lse)
+    args = _lib.FwdArgs(
+        q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), o=o.data_ptr(), lse=lse_ptr,
+        q_stride=_lib.strides_thd(q), k_stride=_lib.strides_thd(k), v_stride=_lib.strides_thd(v),
+        o_stride=_lib.strides_thd(o), lse_stride=_lib._i64x3(0, lse.stride(0), lse.stride(1)),
+        cu_seqlens_q=cu_q.data_ptr(), cu_seqlens_k=cu_k.data_ptr(),
+        dtype=_lib.TORCH_TO_LSFA[q.dtype], batch=cu_q.numel() - 1, heads_q=Hq, heads_kv=k.shape[1],
+        seqlen_q=max_q, seqlen_k=max_k, head_dim=D, causal=int(causal), sm_scale=1.0 / math.sqrt(D), reserved=0)
+    with torch.cuda.device(q.device):
+        _lib.fwd(args, _lib.current_stream(q.device))
+    torch.cuda.synchronize()
+    return o, lse
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,causal", [(64, 8, 2, True), (65, 8, 2, True), (40, 6, 3, False),
+                                              (23, 16, 4, True), (1, 24, 8, True)])
+def test_varlen_every_item_once(gpu, B, Hq, Hkv, causal):
+    """Batches of up to 64 sequences take their (sequence, query tile) items
+    longest-first, found per workgroup from cu_seqlens; longer batches keep
+    the head-major order. Lengths mix empty chunks, chunks longer than their
+    keys, and tile-edge sizes; query heads are or are not a multiple of the
+    8 XCDs. Every output row must be written once and match the oracle."""
+    print(f"case varlen order B={B} Hq={Hq} Hkv={Hkv} causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(B * 100 + Hq)
+    choices_q = [0, 1, 64, 127, 128, 129, 200, 256, 300]
+    lens_q = [choices_q[int(i)] for i in torch.randint(0, len(choices_q), (B,), generator=g)]
+    lens_k = [max(0, lq + int(d)) for lq, d in zip(lens_q, torch.randint(-150, 500, (B,), generator=g))]
+    if B == 1:
+        lens_q, lens_k = [300], [1100]
+    cu_q = torch.tensor([0] + torch.tensor(lens_q).cumsum(0).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + torch.tensor(lens_k).cumsum(0).tolist(), dtype=torch.int32)
+    D = 64
+    q = torch.randn(int(cu_q[-1]), Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).to(torch.bfloat16)
+    o, lse = _varlen_poisoned(q.to(gpu), k.to(gpu), v.to(gpu), cu_q.to(gpu), cu_k.to(gpu),
+                              max(lens_q), max(lens_k), causal)
+    assert not torch.isnan(o).any(), "output rows left unwritten"
+    assert not torch.isnan(lse).any(), "lse rows left unwritten"
+    o_ref, lse_ref = varlen_reference(q, k, v, cu_q, cu_k, causal=causal)
+    assert_gate(o.cpu(), o_ref, f"varlen order B={B}")
+    assert_lse(lse.cpu(), lse_ref, f"varlen order B={B}")
