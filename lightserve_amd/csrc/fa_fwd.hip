@@ -278,6 +278,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   auto kbuf = [&](int t) { return sbytes + (t & 1) * TILE * 2; };
   auto vbuf = [&](int t) { return sbytes + (2 + (t & 1)) * TILE * 2; };
 
+  // LDS operand reads run this many MFMAs ahead of the MFMA that takes them
+  // (the compiler's own order reads only one or two ahead, so every pair of
+  // MFMAs waited out a full LDS latency).
+  constexpr int kReadAhead = 4;
   // S^T = K Q^T for one tile (fp32, unscaled).
   auto scores = [&](const LDS_AS char* Ks, f32x16* s) {
 #pragma unroll
@@ -289,6 +293,14 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
         const X8 a = *(const LDS_AS X8*)(Ks + kb * 32 * DP * 2 + koff[kk]);
         s[kb] = mfma32(a, qreg[kk], s[kb]);
       }
+    }
+    constexpr int NM = KSTEPS * KB;
+#pragma unroll
+    for (int i = 0; i < kReadAhead; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // K reads
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA j
+      if (j + kReadAhead < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
   };
   // Row max of a tile in log2 units (both lane halves hold the row's keys).
@@ -362,6 +374,14 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
                                   lds_read_tr((const LDS_AS T*)(base + voff[dt][1])));
         acc[dt] = mfma32(a, pb[ks], acc[dt]);
       }
+    }
+    constexpr int NM = DT * 2 * KB;
+#pragma unroll
+    for (int i = 0; i < kReadAhead; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // V^T reads
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA j
+      if (j + kReadAhead < NM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
   };
 
