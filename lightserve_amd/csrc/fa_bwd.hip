@@ -214,6 +214,18 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
           dp[kb] = mfma32(*(const LDS_AS X8*)(Vs + o), doreg[kk], dp[kb]);
         }
       }
+      // K / V operand reads run 8 MFMAs ahead of their MFMA (the compiler's
+      // order reads one ahead and waits out an LDS latency per MFMA).
+      {
+        constexpr int NM = 2 * KSTEPS * KB, RA = 8;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (m + RA < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -236,6 +248,17 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
           const X8 a = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(base + troff[dt][0])),
                                     lds_read_tr((const LDS_AS T*)(base + troff[dt][1])));
           acc[dt] = mfma32(a, pack8<T>(s[ks >> 1], 8 * (ks & 1)), acc[dt]);
+        }
+      }
+      // K^T transpose reads run 4 MFMAs ahead.
+      {
+        constexpr int NM = DT * 2 * KB, RA = 4;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (m + RA < NM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
       }
     }
