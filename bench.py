@@ -27,6 +27,7 @@ and scaled linearly to the full job.
 """
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -48,11 +49,12 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
     ap.add_argument("--workload", default="attention",
-                    choices=["attention", "decode", "prefill", "rope", "rmsnorm", "gemv"],
+                    choices=["attention", "decode", "prefill", "rope", "rmsnorm", "gemv", "sweep"],
                     help="attention: a benchmark config 2-5 (default 3); decode: a paged-KV decode step; "
                          "prefill: config 5's chunks over a paged KV cache; "
                          "rope: in-place RoPE of config 3's q and k projections; "
-                         "rmsnorm: fused residual add + RMSNorm, [2048, 8192] bf16")
+                         "rmsnorm: fused residual add + RMSNorm, [2048, 8192] bf16; "
+                         "sweep: B=1 H=32 D=128 bf16 over N 512-8192 beside torch's SDPA")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-parity", action="store_true",
                     help="skip the oracle re-check before timing (profiler runs only, whose per-kernel counters "
@@ -732,6 +734,130 @@ def bench_gemv(args):
     }), flush=True)
 
 
+def bench_sweep(args):
+    """Attention sweep beside the vendor kernel on the same GPU, as the
+    reference's kernels/benchmark_flash_attention.py:36-110 does: B=1, H=32,
+    D=128, bf16, N = 512 ... 8192, causal and not. "vendor" is torch's own
+    scaled_dot_product_attention forced onto its flash backend (the
+    memory-efficient backend if flash cannot run; the line names which).
+    Forward: the inference entry point (flash_attention_forward, no
+    logsumexp) against SDPA; forward+backward: the training pair
+    (forward with L, lsfa_bwd) against SDPA under autograd. Outputs and
+    gradients are compared with the vendor's before each shape is timed.
+    Timing: 10 warm-up calls, then the median of 5 blocks of 30 calls
+    (HIP events)."""
+    import statistics
+    import torch
+    import torch.nn.functional as F
+    from lightserve_amd.kernels.flash_attention import flash_attention_forward
+    from lightserve_amd.kernels.flash_attention_backward import _flash_attention_backward, _flash_attention_forward_lse
+    from lightserve_amd.workloads import bwd_flops, fwd_flops
+    dev = torch.device("cuda", 0)
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+    except ImportError:  # pragma: no cover - torch without the context manager
+        SDPBackend = sdpa_kernel = None
+
+    def vendor(q, k, v, causal, backend):
+        with sdpa_kernel(backend):
+            return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+    def timed(fn, warmup=10, iters=30, repeats=5):
+        for _ in range(warmup):
+            fn()
+        blocks = []
+        for _ in range(repeats):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            blocks.append(e0.elapsed_time(e1) / iters)
+        return statistics.median(blocks)
+
+    B, H, D = 1, 32, 128
+    rows = []
+    backend_used = None
+    t_start = time.time()
+    for n in (512, 1024, 2048, 4096, 8192):
+        for causal in (False, True):
+            g = torch.Generator(device="cpu").manual_seed(n + int(causal))
+            q, k, v, do = (torch.randn(B, H, n, D, generator=g).to(dev, torch.bfloat16) for _ in range(4))
+            row = {"shape": f"{B}x{H}x{n}x{D}", "causal": causal}
+            ours = flash_attention_forward(q, k, v, causal=causal)
+            ref = None
+            for be in ((SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION) if SDPBackend else ()):
+                try:
+                    ref = vendor(q, k, v, causal, be)
+                    backend_used = backend_used or str(be).split(".")[-1]
+                    vbe = be
+                    break
+                except RuntimeError:
+                    continue
+            if ref is not None:
+                err = (ours.float() - ref.float()).abs().max().item()
+                row["fwd_max_abs_vs_vendor"] = round(err, 5)
+                row["fwd_ok"] = err <= 2e-2
+            f_fwd = fwd_flops(B, H, n, D, causal)
+            ms = timed(lambda: flash_attention_forward(q, k, v, causal=causal))
+            row["fwd_ms"] = round(ms, 5)
+            row["fwd_tflops"] = round(f_fwd / (ms * 1e-3) / 1e12, 2)
+            if ref is not None:
+                vms = timed(lambda: vendor(q, k, v, causal, vbe))
+                row["vendor_fwd_ms"] = round(vms, 5)
+                row["vendor_fwd_tflops"] = round(f_fwd / (vms * 1e-3) / 1e12, 2)
+                row["fwd_pct_of_vendor"] = round(100 * vms / ms, 1)
+            row["fwd_pct_of_peak"] = round(100 * row["fwd_tflops"] / PEAK_BF16_TFLOPS, 2)
+
+            # forward + backward
+            f_step = f_fwd + bwd_flops(B, H, n, D, causal)
+
+            def ours_step():
+                o, lse = _flash_attention_forward_lse(q, k, v, causal)
+                return _flash_attention_backward(do, q, k, v, o, lse, causal)
+            dq, dk, dv = ours_step()
+            if ref is not None:
+                qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+
+                def vendor_step():
+                    qg.grad = kg.grad = vg.grad = None
+                    vendor(qg, kg, vg, causal, vbe).backward(do)
+                vendor_step()
+                gerr = max((a.float() - b.grad.float()).abs().max().item() for a, b in ((dq, qg), (dk, kg), (dv, vg)))
+                row["grad_max_abs_vs_vendor"] = round(gerr, 5)
+                row["grad_ok"] = gerr <= 5e-2
+            ms = timed(ours_step)
+            row["fwd_bwd_ms"] = round(ms, 5)
+            row["fwd_bwd_tflops"] = round(f_step / (ms * 1e-3) / 1e12, 2)
+            if ref is not None:
+                vms = timed(vendor_step)
+                row["vendor_fwd_bwd_ms"] = round(vms, 5)
+                row["vendor_fwd_bwd_tflops"] = round(f_step / (vms * 1e-3) / 1e12, 2)
+                row["fwd_bwd_pct_of_vendor"] = round(100 * vms / ms, 1)
+            row["fwd_bwd_pct_of_peak"] = round(100 * row["fwd_bwd_tflops"] / PEAK_BF16_TFLOPS, 2)
+            rows.append(row)
+            print(f"sweep {row['shape']} causal={causal}: fwd {row['fwd_tflops']} TF/s "
+                  f"({row.get('fwd_pct_of_vendor', '-')}% of vendor), fwd+bwd {row['fwd_bwd_tflops']} TF/s "
+                  f"({row.get('fwd_bwd_pct_of_vendor', '-')}% of vendor)", file=sys.stderr, flush=True)
+            del q, k, v, do, ours, ref
+    gm = math.exp(sum(math.log(r["fwd_tflops"]) for r in rows) / len(rows))
+    ok = all(r.get("fwd_ok", True) and r.get("grad_ok", True) for r in rows)
+    result = {
+        "metric": "attention sweep B=1 H=32 D=128 bf16, N 512-8192: geometric-mean forward TFLOP/s",
+        "value": round(gm, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": 150, "warmup": 10,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic, seeded per shape, inputs resident in HBM",
+        "config": {"workload": "sweep over the reference's kernels/benchmark_flash_attention.py shapes"},
+        "vendor": {"kernel": "torch.nn.functional.scaled_dot_product_attention", "backend": backend_used,
+                   "torch": torch.__version__},
+        "parity": {"ok": ok, "against": "vendor outputs and gradients (fwd max-abs <= 2e-2, grads <= 5e-2)"},
+        "wall_s": round(time.time() - t_start, 1),
+        "sweep": rows,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -749,6 +875,9 @@ def main():
         return
     if args.workload == "prefill":
         bench_prefill(args)
+        return
+    if args.workload == "sweep":
+        bench_sweep(args)
         return
     if args.workload == "gemv":
         bench_gemv(args)
