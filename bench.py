@@ -12,10 +12,12 @@ region. FLOPs follow the reference's convention
 kernels/benchmark_flash_attention_backward.py:65-68): F_fwd = 4*B*H*N^2*D,
 halved when causal; F_bwd = 2.5*F_fwd; a fwd+bwd step counts 3.5*F_fwd.
 
-Timing: W untimed warm-up steps; then K steps bracketed by
-torch.cuda.synchronize() on both sides; HIP events on the launch stream
-around each phase give the per-phase (per-launch) kernel time used for the
-forward TFLOP/s and the roofline. Correctness is re-checked against the
+Timing: W untimed warm-up steps; then K steps back to back, bracketed by
+torch.cuda.synchronize() on both sides, with one pair of HIP events on the
+launch stream around them (ms_per_step = their interval / K). For training
+steps a second pass with an event between the forward and the backward of
+each step gives the forward's share; forward-only steps take the forward
+time from the timed region itself. Correctness is re-checked against the
 oracle on every (batch, head) slice before timing, as the reference does
 (kernels/benchmark_flash_attention.py:104-106): o and lse, and dq/dk/dv when
 the step has a backward, all gated.
@@ -964,26 +966,39 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # Timed region: exactly --steps steps back to back, one event pair around
+    # them (per-step events would count the host's time to enqueue a step
+    # whenever the GPU drains the queue, which short forward-only steps do).
+    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        e0, e1, e2 = ev[i]
-        e0.record(stream)
-        o, lse = fwd()
-        e1.record(stream)
-        if bwd is not None:
-            bwd(o, lse)
-        e2.record(stream)
+    h0.record(stream)
+    for _ in range(args.steps):
+        step()
+    h1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    fwd_ms = [a.elapsed_time(b) for a, b, _ in ev]
-    bwd_ms = [b.elapsed_time(c) for _, b, c in ev]
-    step_ms = [a.elapsed_time(c) for a, _, c in ev]
-    ms_per_step = sum(step_ms) / len(step_ms)
+    ms_per_step = h0.elapsed_time(h1) / args.steps
     value = f_step / (ms_per_step * 1e-3) / 1e12
-    fwd_avg = sum(fwd_ms) / len(fwd_ms)
+    if bwd is None:
+        fwd_avg, bwd_ms = ms_per_step, None
+    else:
+        # forward / backward split of a training step: a second pass with an
+        # event between the two halves of every step
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+               torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            e0, e1, e2 = ev[i]
+            e0.record(stream)
+            o, lse = fwd()
+            e1.record(stream)
+            bwd(o, lse)
+            e2.record(stream)
+        torch.cuda.synchronize()
+        fwd_ms = [a.elapsed_time(b) for a, b, _ in ev]
+        bwd_ms = [b.elapsed_time(c) for _, b, c in ev]
+        fwd_avg = sum(fwd_ms) / len(fwd_ms)
     fwd_tflops = f_fwd / (fwd_avg * 1e-3) / 1e12
 
     wl_key = f"config{args.config}"
