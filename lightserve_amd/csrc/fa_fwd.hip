@@ -268,9 +268,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
-  // l_run: sum of the rounded p the PV products take (normalises O, so the
-  // weights of the V rows sum to one exactly); l_lse: sum of the fp32 p
-  // (kept only for the logsumexp output, as the reference's l_i).
+  // l_run: the sum O is normalised by (bf16: of the rounded p the PV products
+  // take, so the weights of the V rows sum to one exactly; fp16: of the fp32
+  // p); l_lse: sum of the fp32 p (for the logsumexp output, as the
+  // reference's l_i).
   float m_run = -1e30f, l_run = 0.f, l_lse = 0.f;
   const float kTileSumMax = __builtin_exp2f(kMaxLog2P<T>);
 
@@ -315,9 +316,15 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   };
   // Exponentials with the current offset, rounded to the input dtype into
   // the PV operands; returns this lane's part of the tile's row sums: x = the
-  // rounded p (v_dot2 with ones), y = the fp32 p with LSE (four interleaved
-  // partial sums), else 0. s is left as it is.
+  // sum O is normalised by, y = the fp32 p with LSE (four interleaved partial
+  // sums), else 0. s is left as it is. For bf16, x sums the rounded p
+  // (v_dot2 with ones), so that O's weights sum to one exactly (8-bit
+  // mantissas: normalising by the fp32 sum fails the max-abs gate when one
+  // large p dominates a row). fp16 keeps 11 bits, so the fp32 sum moves O by
+  // at most ~2^-11 |v|; it is used for x as well, which drops the 16 v_dot2
+  // per tile (a v_dot2 holds up the other wave's MFMAs on the SIMD).
   auto softmax = [&](const f32x16* s, X8* pb) -> float2 {
+    constexpr bool kF16 = std::is_same<T, _Float16>::value;
     const float neg_m = -m_run;
     float rs[4] = {0.f, 0.f, 0.f, 0.f}, re[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -326,16 +333,18 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         p[i] = fast_exp2(fmaf(s[kb][i], sl2, neg_m));
-        if constexpr (LSE) re[i & 3] += p[i];
+        if constexpr (LSE || kF16) re[i & 3] += p[i];
       }
       pb[2 * kb] = pack8<T>(p, 0);
       pb[2 * kb + 1] = pack8<T>(p, 8);
-      sum8_into(pb[2 * kb], rs);
-      sum8_into(pb[2 * kb + 1], rs);
+      if constexpr (!kF16) {
+        sum8_into(pb[2 * kb], rs);
+        sum8_into(pb[2 * kb + 1], rs);
+      }
     }
     float2 r;
-    r.x = (rs[0] + rs[1]) + (rs[2] + rs[3]);
-    r.y = LSE ? (re[0] + re[1]) + (re[2] + re[3]) : 0.f;
+    r.y = (LSE || kF16) ? (re[0] + re[1]) + (re[2] + re[3]) : 0.f;
+    r.x = kF16 ? r.y : (rs[0] + rs[1]) + (rs[2] + rs[3]);
     return r;
   };
   auto add_sums = [&](float2 ts) {
