@@ -21,7 +21,9 @@
 //   workgroup = 4 waves = 128 query rows of one (batch, head); wave w owns
 //   rows 32w..32w+31, one row per lane pair (l, l+32). At most 256 registers
 //   per wave, so two workgroups share a CU and the hardware interleaves one
-//   wave's softmax with the other's MFMA work on each SIMD.
+//   wave's softmax with the other's MFMA work on each SIMD. Long dense
+//   sequences take 8-wave workgroups (256 rows, one per CU), which halve the
+//   K/V bytes streamed into LDS per query row.
 //   K/V tiles of 64 keys go global -> LDS with buffer_load ... lds (no
 //   register staging; rows past the sequence read as zero through the buffer
 //   range check), double-buffered, 16-byte segments XOR-swizzled per row.
@@ -115,11 +117,15 @@ __device__ __forceinline__ void varlen_item_at(const FwdParams& p, int rank, int
   qt_out = __builtin_amdgcn_readfirstlane(__shfl(tq - a_hi + k - pre, src));
 }
 
-template <typename T, int DP, bool CAUSAL, bool VARLEN, bool LSE, bool PAGED>
-__global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
+// NW waves per workgroup (NW x 32 query rows): 4 (two workgroups per CU) or,
+// for long dense sequences, 8 (one per CU), so that every K/V tile brought
+// into LDS serves twice the rows.
+template <typename T, int DP, bool CAUSAL, bool VARLEN, bool LSE, bool PAGED, int NW>
+__global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
-  constexpr int NW = 4, BM = NW * 32, BN = 64;
+  constexpr int BM = NW * 32, BN = 64;
+  static_assert(NW == 4 || (NW == 8 && !VARLEN && !PAGED), "8 waves for dense launches only");
   constexpr int TILE = BN * DP;              // elements of one K or V tile
   constexpr int LDI = TILE * 2 / 1024 / NW;  // 1 KB direct loads per wave per tile
   constexpr int KSTEPS = DP / 16;
@@ -127,7 +133,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   constexpr int KB = BN / 32;
   static_assert(LDI >= 1, "tile too small for the workgroup");
   static_assert(!PAGED || VARLEN, "paged K/V takes packed varlen queries");
-  static_assert(LDI * 1024 == 16 * DP * 2, "each wave loads 16 rows of a tile");
+  static_assert(!PAGED || LDI * 1024 == 16 * DP * 2, "each wave loads 16 rows of a tile");
 
   __shared__ __attribute__((aligned(1024))) T smem_raw[4 * TILE];  // K0 K1 V0 V1
   LDS_AS T* smem = (LDS_AS T*)smem_raw;
@@ -497,14 +503,26 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const FwdParams p) {
   }
 }
 
-template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED = false>
-static hipError_t launch_fwd(const FwdParams& p, hipStream_t s) {
+template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED, int NW>
+static hipError_t launch_fwd_nw(FwdParams p, hipStream_t s) {
+  p.num_q_tiles = (p.Nq + NW * 32 - 1) / (NW * 32);
   const int total = p.num_q_tiles * p.B * p.Hq;
   if (p.lse != nullptr)
-    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, true, PAGED>), dim3(total), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, true, PAGED, NW>), dim3(total), dim3(NW * 64), 0, s, p);
   else
-    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, false, PAGED>), dim3(total), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fa_fwd_kernel<T, DP, CAUSAL, VARLEN, false, PAGED, NW>), dim3(total), dim3(NW * 64), 0, s, p);
   return hipGetLastError();
+}
+
+// 8-wave workgroups for dense launches with head dims of 64 or more and at
+// least 4096 queries (measured: config-3 shape -3%, non-causal N=4096 -6%,
+// but +2% at N=2048, where one workgroup per CU leaves a longer causal tail).
+template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED = false>
+static hipError_t launch_fwd(const FwdParams& p, hipStream_t s) {
+  if constexpr (!VARLEN && !PAGED && DP >= 64) {
+    if (p.Nq >= 4096) return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);
+  }
+  return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 4>(p, s);
 }
 
 template <typename T, int DP>
@@ -525,7 +543,6 @@ static hipError_t dispatch_fwd_t(const FwdParams& p, int dp, bool causal, bool v
 // Host entry used by the C ABI layer. is_bf16 selects bf16 vs fp16 operands;
 // dp is the padded head dim (32, 64 or 128). Query tiles are 128 rows.
 hipError_t fwd_mfma(FwdParams p, bool is_bf16, int dp, bool causal, bool varlen, hipStream_t s) {
-  p.num_q_tiles = (p.Nq + 127) / 128;
   p.heads_per_group = heads_per_group_for((long long)p.Nk * dp * 2 * 2);  // K and V rows of a head
   if (is_bf16) return dispatch_fwd_t<__bf16>(p, dp, causal, varlen, s);
   return dispatch_fwd_t<_Float16>(p, dp, causal, varlen, s);
@@ -548,7 +565,6 @@ static hipError_t dispatch_paged_t(const FwdParams& p, int dp, bool causal, hipS
 // Paged K/V forward (arguments validated by the C ABI layer; p.Nq is the
 // longest query chunk, block_shift >= 4).
 hipError_t fwd_paged(FwdParams p, bool is_bf16, int dp, bool causal, hipStream_t s) {
-  p.num_q_tiles = (p.Nq + 127) / 128;
   p.heads_per_group = heads_per_group_for((long long)p.Nk * dp * 2 * 2);
   if (is_bf16) return dispatch_paged_t<__bf16>(p, dp, causal, s);
   return dispatch_paged_t<_Float16>(p, dp, causal, s);
