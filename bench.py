@@ -12,7 +12,10 @@ region. FLOPs follow the reference's convention
 kernels/benchmark_flash_attention_backward.py:65-68): F_fwd = 4*B*H*N^2*D,
 halved when causal; F_bwd = 2.5*F_fwd; a fwd+bwd step counts 3.5*F_fwd.
 
-Timing: W untimed warm-up steps; then K steps back to back, bracketed by
+Timing: W untimed warm-up steps, continued (untimed) until at least 200 ms
+of GPU work has gone into the warm-up (the reference's do_bench also warms up
+by time; an MI355X coming out of idle runs short kernels up to ~20% slower
+until tens of ms of sustained load have passed); then K steps back to back, bracketed by
 torch.cuda.synchronize() on both sides, with one pair of HIP events on the
 launch stream around them (ms_per_step = their interval / K). For training
 steps a second pass with an event between the forward and the backward of
@@ -42,6 +45,30 @@ PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16/fp16 MFMA: 256 CU x 2.4 GHz x 409
 HBM_PEAK_GBS = 8000.0
 METRIC = "attention TFLOP/s fwd & fwd+bwd, % of MI355X bf16 MFMA peak, 1 GPU"
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.txt")
+
+
+WARM_MS = 200.0
+
+
+def warm_up(fn, n, stream=None, min_ms=WARM_MS, cap=200000):
+    """Runs fn() n times, then more, untimed, until at least min_ms of GPU time
+    has gone into the warm-up. Returns the number of calls made."""
+    import torch
+
+    done, runs, batch = 0.0, 0, max(1, n)
+    while True:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(batch):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        done += e0.elapsed_time(e1)
+        runs += batch
+        if done >= min_ms or runs >= cap:
+            return runs
+        per = max(done / runs, 1e-3)
+        batch = min(cap - runs, max(1, int(math.ceil((min_ms - done) / per))))
 
 
 def parse_args():
@@ -248,8 +275,7 @@ def bench_decode(args):
     parity_ok = worst["o"][0] <= 2e-2 and worst["o"][1] <= 2e-3 and worst["lse"][0] <= 1e-3
 
     calibration_copy(dev, args.calibrate_copy)
-    for _ in range(args.warmup):
-        step()
+    warm_runs = warm_up(step, args.warmup)
     # A decode step lasts ~0.1 ms, so the steps are enqueued back to back
     # between one event pair (as a serving loop issues them): per-step event
     # pairs would count the host's Python time before each launch.
@@ -272,7 +298,7 @@ def bench_decode(args):
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     result = {
         "metric": "paged-KV decode attention: algorithmic HBM GB/s (K/V streamed), 1 GPU",
-        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup, "warmup_calls": warm_runs,
         "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": f"synthetic, seeded (seed {c['seed']}), cache resident in HBM",
         "config": {"workload": (f"decode: B={B} Hq={Hq} Hkv={Hkv} D={D} block_size={bs} "
@@ -335,8 +361,7 @@ def bench_rope(args):
     qr, kr = apply_rope(q0, k0, cos.double().cpu(), sin.double().cpu(), N)
     err = max((qv[:1, :1].double().cpu() - qr).abs().max().item(), (kv[:1, :1].double().cpu() - kr).abs().max().item())
     calibration_copy(dev, args.calibrate_copy)
-    for _ in range(args.warmup):
-        apply_rope_(qv, kv, cos, sin)
+    warm_runs = warm_up(lambda: apply_rope_(qv, kv, cos, sin), args.warmup)
     stream = torch.cuda.current_stream(dev)
     steps = max(args.steps, 200)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -353,7 +378,7 @@ def bench_rope(args):
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     print(json.dumps({
         "metric": "RoPE of q and k in place: algorithmic HBM GB/s, 1 GPU", "value": round(gbs, 1), "unit": "GB/s",
-        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "warmup_calls": warm_runs, "ms_per_step": round(ms, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic, seeded (seed 2), resident in HBM",
         "config": {"workload": f"rope: q [{B},{N},{Hq},{D}] and k [{B},{N},{Hkv},{D}] bf16 as [B,H,N,D] views",
                    "bytes_per_step": alg_bytes},
@@ -449,8 +474,7 @@ def bench_prefill(args):
     calibration_copy(dev, args.calibrate_copy)
 
     def timed(fn, n):
-        for _ in range(args.warmup):
-            fn()
+        warm_up(fn, args.warmup, stream)
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         s.record(stream)
@@ -552,8 +576,7 @@ def bench_rmsnorm(args):
     stream = torch.cuda.current_stream(dev)
     sptr = stream.cuda_stream
     calibration_copy(dev, args.calibrate_copy)
-    for _ in range(args.warmup):
-        _lib.rmsnorm(args_c, sptr)
+    warm_runs = warm_up(lambda: _lib.rmsnorm(args_c, sptr), args.warmup, stream)
     steps = max(args.steps, 200)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -607,7 +630,7 @@ def bench_rmsnorm(args):
                                           f"workload, median of 5: {tc * 1e3:.1f} ms")}
     print(json.dumps({
         "metric": "fused add + RMSNorm: algorithmic HBM GB/s, 1 GPU", "value": round(gbs, 1), "unit": "GB/s",
-        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "warmup_calls": warm_runs, "ms_per_step": round(ms, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic, seeded (seed 3), resident in HBM",
         "config": {"workload": f"rmsnorm: fused_add_rmsnorm x, residual [{M},{N}] bf16, eps {eps}",
                    "bytes_per_step": alg_bytes},
@@ -663,8 +686,7 @@ def bench_gemv(args):
     stream = torch.cuda.current_stream(dev)
     sptr = stream.cuda_stream
     calibration_copy(dev, args.calibrate_copy)
-    for _ in range(args.warmup):
-        _lib.gemv(args_c, sptr)
+    warm_runs = warm_up(lambda: _lib.gemv(args_c, sptr), args.warmup, stream)
     steps = max(args.steps, 100)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -720,7 +742,7 @@ def bench_gemv(args):
                                           "GB/s counts the bf16 weight bytes")}
     print(json.dumps({
         "metric": "decode skinny GEMM (lm_head): algorithmic HBM GB/s, 1 GPU", "value": round(gbs, 1),
-        "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup, "warmup_calls": warm_runs, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic, seeded (seed 5), resident in HBM",
         "config": {"workload": f"gemv: x [{M},{K}] @ W [{K},{N}] bf16 (LLaMA-3-8B lm_head at batch 1)",
@@ -765,8 +787,7 @@ def bench_sweep(args):
             return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
 
     def timed(fn, warmup=10, iters=30, repeats=5):
-        for _ in range(warmup):
-            fn()
+        warm_up(fn, warmup, min_ms=50.0)
         blocks = []
         for _ in range(repeats):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -962,9 +983,7 @@ def main():
 
     calibration_copy(dev, args.calibrate_copy)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_runs = warm_up(step, args.warmup, stream)
 
     # Timed region: exactly --steps steps back to back, one event pair around
     # them (per-step events would count the host's time to enqueue a step
@@ -1068,7 +1087,7 @@ def main():
                 "kernels": kernels}
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "steps": args.steps, "warmup": args.warmup, "warmup_calls": warm_runs, "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16" if q.dtype == torch.bfloat16 else ("fp16" if q.dtype == torch.float16 else "fp32"),
         "data": f"synthetic, seeded (seed {cfg['seed']}), inputs resident in HBM",

@@ -22,8 +22,9 @@
 //   rows 32w..32w+31, one row per lane pair (l, l+32). At most 256 registers
 //   per wave, so two workgroups share a CU and the hardware interleaves one
 //   wave's softmax with the other's MFMA work on each SIMD. Long dense
-//   sequences take 8-wave workgroups (256 rows, one per CU), which halve the
-//   K/V bytes streamed into LDS per query row.
+//   sequences and varlen batches with long query runs take 8-wave
+//   workgroups (256 rows, one per CU), which halve the K/V bytes streamed
+//   into LDS per query row.
 //   K/V tiles of 64 keys go global -> LDS with buffer_load ... lds (no
 //   register staging; rows past the sequence read as zero through the buffer
 //   range check), double-buffered, 16-byte segments XOR-swizzled per row.
@@ -34,8 +35,9 @@
 //
 // Paged K/V (PAGED, with packed varlen queries): the keys of sequence b are
 // its seq_lens_k[b] cache slots, found through its block-table row. A 64-key
-// tile is loaded as four 16-row pieces, one per wave; with block sizes that
-// are multiples of 16 each piece lies inside one cache block, so every wave
+// tile is loaded as one 16-row (4 waves) or 8-row (8 waves) piece per wave;
+// with block sizes that are multiples of 16 each piece lies inside one cache
+// block, so every wave
 // builds one buffer descriptor per tile from one block-table entry and the
 // LDS tile is the same as for contiguous K/V. Block ids outside
 // [0, num_blocks) read as zeros.
@@ -55,17 +57,17 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
-// Number of a sequence's query tiles (tq of them, 128 rows each) whose key
+// Number of a sequence's query tiles (tq of them, BM rows each) whose key
 // tile count (64 keys each) exceeds x; the tiles counted are always the last
 // ones, as causal work grows with the tile index. x = -1 counts every tile.
-template <bool CAUSAL>
+template <bool CAUSAL, int BM>
 __device__ __forceinline__ int tiles_above(int x, int tq, int nk, int off) {
   if (x < 0) return tq;
   if (tq == 0 || nk <= 64 * x) return 0;  // the last tile sees all nk keys
   if (!CAUSAL) return tq;
-  // tile t < tq-1 sees off + 128(t+1) keys: more than 64x iff t >= (64x-off)/128
+  // tile t < tq-1 sees off + BM(t+1) keys: more than 64x iff t >= (64x-off)/BM
   const long long y = 64LL * x - off;
-  return y < 0 ? tq : 1 + max(0, tq - 1 - (int)(y >> 7));
+  return y < 0 ? tq : 1 + max(0, tq - 1 - (int)(y / BM));
 }
 
 // Longest-first order of a varlen launch's (sequence, query tile) items, so
@@ -76,14 +78,14 @@ __device__ __forceinline__ int tiles_above(int x, int tq, int nk, int off) {
 // rank is found by binary search on the number of items above a count, then
 // the item among those of that count by a prefix sum over the sequences.
 // Wave-uniform result.
-template <bool CAUSAL, bool PAGED>
+template <bool CAUSAL, bool PAGED, int BM>
 __device__ __forceinline__ void varlen_item_at(const FwdParams& p, int rank, int lane, int& b_out, int& qt_out) {
   int tq = 0, nk = 0, off = 0;
   if (lane < p.B) {
     const int nq = p.cu_q[lane + 1] - p.cu_q[lane];
     nk = PAGED ? min(max(p.seq_lens_k[lane], 0), p.max_blocks << p.block_shift)
                : p.cu_k[lane + 1] - p.cu_k[lane];
-    tq = nq > 0 ? (nq + 127) >> 7 : 0;
+    tq = nq > 0 ? (nq + BM - 1) / BM : 0;
     off = nk - nq;
   }
   b_out = -1;
@@ -95,13 +97,13 @@ __device__ __forceinline__ void varlen_item_at(const FwdParams& p, int rank, int
   int lo = 0, hi = __builtin_amdgcn_readfirstlane(kmax);  // no item exceeds hi
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    if (__builtin_amdgcn_readfirstlane(wave_sum_i(tiles_above<CAUSAL>(mid, tq, nk, off))) <= rank) hi = mid;
+    if (__builtin_amdgcn_readfirstlane(wave_sum_i(tiles_above<CAUSAL, BM>(mid, tq, nk, off))) <= rank) hi = mid;
     else lo = mid + 1;
   }
   // rank lies among the items of exactly lo key tiles: tiles
   // [tq - above(lo-1), tq - above(lo)) of each sequence.
-  const int a_hi = tiles_above<CAUSAL>(lo - 1, tq, nk, off);
-  const int a_lo = tiles_above<CAUSAL>(lo, tq, nk, off);
+  const int a_hi = tiles_above<CAUSAL, BM>(lo - 1, tq, nk, off);
+  const int a_lo = tiles_above<CAUSAL, BM>(lo, tq, nk, off);
   const int c = a_hi - a_lo;
   const int k = rank - __builtin_amdgcn_readfirstlane(wave_sum_i(a_lo));
   int inc = c;
@@ -118,14 +120,15 @@ __device__ __forceinline__ void varlen_item_at(const FwdParams& p, int rank, int
 }
 
 // NW waves per workgroup (NW x 32 query rows): 4 (two workgroups per CU) or,
-// for long dense sequences, 8 (one per CU), so that every K/V tile brought
-// into LDS serves twice the rows.
+// for long dense sequences and varlen batches with long query runs,
+// 8 (one per CU), so that every K/V tile brought into LDS serves twice the
+// rows.
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool LSE, bool PAGED, int NW>
 __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
   constexpr int BM = NW * 32, BN = 64;
-  static_assert(NW == 4 || (NW == 8 && !VARLEN && !PAGED), "8 waves for dense launches only");
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   constexpr int TILE = BN * DP;              // elements of one K or V tile
   constexpr int LDI = TILE * 2 / 1024 / NW;  // 1 KB direct loads per wave per tile
   constexpr int KSTEPS = DP / 16;
@@ -133,7 +136,10 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   constexpr int KB = BN / 32;
   static_assert(LDI >= 1, "tile too small for the workgroup");
   static_assert(!PAGED || VARLEN, "paged K/V takes packed varlen queries");
-  static_assert(!PAGED || LDI * 1024 == 16 * DP * 2, "each wave loads 16 rows of a tile");
+  constexpr int RPW = LDI * 1024 / (DP * 2);  // tile rows each wave loads
+  // Paged: a wave's rows must lie in one cache block (blocks hold 16 or more
+  // tokens, a power of two).
+  static_assert(!PAGED || (RPW * DP * 2 == LDI * 1024 && (RPW == 8 || RPW == 16)), "rows per wave");
 
   __shared__ __attribute__((aligned(1024))) T smem_raw[4 * TILE];  // K0 K1 V0 V1
   LDS_AS T* smem = (LDS_AS T*)smem_raw;
@@ -152,7 +158,7 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
     const int L = blockIdx.x;
     const int rank = L / p.Hq, u = L - rank * p.Hq;
     h = (p.Hq & 7) == 0 ? (u & 7) * (p.Hq >> 3) + (u >> 3) : u;
-    varlen_item_at<CAUSAL, PAGED>(p, rank, lane, b, qt);
+    varlen_item_at<CAUSAL, PAGED, BM>(p, rank, lane, b, qt);
     if (b < 0) return;  // uniform, before any barrier
   } else {
     int bh;
@@ -209,7 +215,7 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   }
 
   // Direct global -> LDS tile load: wave w issues LDI 1 KB chunks (tile rows
-  // 16w..16w+15); lane t of chunk c lands at tile byte (w*LDI + c)*1024 + 16t
+  // RPW w .. RPW w + RPW-1); lane t of chunk c lands at tile byte (w*LDI + c)*1024 + 16t
   // = (row, swizzled seg). The buffer descriptor is rebuilt per tile (scalar
   // work) and clipped to the rows that exist, so the per-lane byte offsets
   // are loop-invariant and rows at or past nk (and columns at or past D) read
@@ -220,18 +226,18 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
     const int byte = (wave * LDI + c) * 1024 + lane * 16;
     const int row = byte / (DP * 2);
     const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
-    const int r = PAGED ? row - 16 * wave : row;
+    const int r = PAGED ? row - RPW * wave : row;
     kvo[c] = seg * 8 < D ? (int)(r * p.skn * 2) + seg * 16 : (int)0x80000000;
     vvo[c] = seg * 8 < D ? (int)(r * p.svn * 2) + seg * 16 : (int)0x80000000;
   }
-  // Paged: the cache block holding this wave's 16 rows of tile j (-1 past
+  // Paged: the cache block holding this wave's RPW rows of tile j (-1 past
   // the sequence). The table is read through the constant address space (it
   // does not change during a launch), so the wave-uniform read is one scalar
   // load into an SGPR, issued one pipelined iteration before the tile load
   // that uses it; it completes under the previous iteration's closing waits.
   auto block_of = [&](int j) -> int {
     if (!PAGED) return 0;
-    const int key0 = j * BN + 16 * wave;  // wave-uniform
+    const int key0 = j * BN + RPW * wave;  // wave-uniform
     if (key0 >= nk) return -1;
     const __attribute__((address_space(4))) int32_t* bt = (const __attribute__((address_space(4))) int32_t*)p.block_tables;
     return bt[(int64_t)b * p.sbt + (key0 >> p.block_shift)];
@@ -240,8 +246,8 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
                        int blk) {
     __amdgpu_buffer_rsrc_t rs;
     if (PAGED) {
-      const int key0 = j * BN + 16 * wave;  // wave-uniform
-      const int rows = min(nk - key0, 16);
+      const int key0 = j * BN + RPW * wave;  // wave-uniform
+      const int rows = min(nk - key0, RPW);
       blk = __builtin_amdgcn_readfirstlane(blk);
       const bool live = rows > 0 && blk >= 0 && blk < p.num_blocks;
       const int slot = key0 & ((1 << p.block_shift) - 1);
@@ -514,13 +520,19 @@ static hipError_t launch_fwd_nw(FwdParams p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// 8-wave workgroups for dense launches with head dims of 64 or more and at
-// least 4096 queries (measured: config-3 shape -3%, non-causal N=4096 -6%,
-// but +2% at N=2048, where one workgroup per CU leaves a longer causal tail).
+// 8-wave workgroups, head dims of 64 or more: dense launches with at least
+// 4096 queries (measured: config-3 shape -3%, non-causal N=4096 -6%, but +2%
+// at N=2048, where one workgroup per CU leaves a longer causal tail), and
+// varlen batches (packed or paged K/V) of up to 64 sequences (the
+// longest-first ranking) with runs of at least 512 queries (config 5,
+// 512-query chunks over 2.4k-7.3k keys: -5%).
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED = false>
 static hipError_t launch_fwd(const FwdParams& p, hipStream_t s) {
   if constexpr (!VARLEN && !PAGED && DP >= 64) {
     if (p.Nq >= 4096) return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);
+  }
+  if constexpr (VARLEN && DP >= 64) {
+    if (p.B <= 64 && p.Nq >= 512) return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);
   }
   return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 4>(p, s);
 }

@@ -86,21 +86,31 @@ def _varlen_poisoned(q, k, v, cu_q, cu_k, max_q, max_k, causal):
     return o, lse
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,causal", [(64, 8, 2, True), (65, 8, 2, True), (40, 6, 3, False),
-                                              (23, 16, 4, True), (1, 24, 8, True)])
-def test_varlen_every_item_once(gpu, B, Hq, Hkv, causal):
+@pytest.mark.parametrize("B,Hq,Hkv,causal,long_q", [(64, 8, 2, True, False), (65, 8, 2, True, False),
+                                                     (40, 6, 3, False, False), (23, 16, 4, True, False),
+                                                     (1, 24, 8, True, False), (64, 8, 2, True, True),
+                                                     (65, 8, 2, True, True), (23, 16, 4, True, True),
+                                                     (40, 6, 3, False, True)])
+def test_varlen_every_item_once(gpu, B, Hq, Hkv, causal, long_q):
     """Batches of up to 64 sequences take their (sequence, query tile) items
     longest-first, found per workgroup from cu_seqlens; longer batches keep
     the head-major order. Lengths mix empty chunks, chunks longer than their
     keys, and tile-edge sizes; query heads are or are not a multiple of the
-    8 XCDs. Every output row must be written once and match the oracle."""
-    print(f"case varlen order B={B} Hq={Hq} Hkv={Hkv} causal={causal}", flush=True)
-    g = torch.Generator().manual_seed(B * 100 + Hq)
+    8 XCDs. With runs of 512 queries or more (long_q) batches of up to 64
+    sequences take 256-row tiles (8-wave workgroups), so the lengths also
+    straddle 256-row edges. Every output row must be written once and match
+    the oracle."""
+    print(f"case varlen order B={B} Hq={Hq} Hkv={Hkv} causal={causal} long_q={long_q}", flush=True)
+    g = torch.Generator().manual_seed(B * 100 + Hq + (7 if long_q else 0))
     choices_q = [0, 1, 64, 127, 128, 129, 200, 256, 300]
+    if long_q:
+        choices_q = [0, 1, 129, 255, 256, 257, 511, 512, 700]
     lens_q = [choices_q[int(i)] for i in torch.randint(0, len(choices_q), (B,), generator=g)]
     lens_k = [max(0, lq + int(d)) for lq, d in zip(lens_q, torch.randint(-150, 500, (B,), generator=g))]
     if B == 1:
         lens_q, lens_k = [300], [1100]
+    if long_q:
+        lens_q[0] = 700  # at least one run of 512 or more
     cu_q = torch.tensor([0] + torch.tensor(lens_q).cumsum(0).tolist(), dtype=torch.int32)
     cu_k = torch.tensor([0] + torch.tensor(lens_k).cumsum(0).tolist(), dtype=torch.int32)
     D = 64

@@ -63,6 +63,10 @@ def _check(case, label, causal=True, lens_ref=None, **kw):
 
 LENS_K = [300, 17, 1000, 64, 0, 129, 500, 16]
 LENS_Q = [128, 17, 1, 0, 0, 64, 300, 16]
+# Runs of 512 queries or more: batches of up to 64 sequences then take 8-wave
+# workgroups (256-row tiles, 8-row pieces of a cache block per wave).
+LENS_K_LONG = [900, 17, 1000, 64, 0, 600, 1200, 16]
+LENS_Q_LONG = [600, 17, 1, 0, 0, 513, 700, 16]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -73,19 +77,33 @@ def test_prefill_ragged(gpu, hq, hkv, dtype, causal):
     _check(_make_case(LENS_K, LENS_Q, hq, hkv, 128, 16, dtype, seed=hq + hkv), f"hq={hq} hkv={hkv}", causal)
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (12, 4), (32, 4)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_ragged_long_chunks(gpu, hq, hkv, causal):
+    print(f"case prefill ragged long hq={hq} hkv={hkv} causal={causal}", flush=True)
+    _check(_make_case(LENS_K_LONG, LENS_Q_LONG, hq, hkv, 128, 16, torch.bfloat16, seed=40 + hq + hkv),
+           f"long hq={hq} hkv={hkv}", causal)
+
+
 @pytest.mark.parametrize("bs", [16, 32, 64])
 @pytest.mark.parametrize("d", [64, 96, 128])
-def test_prefill_block_sizes_and_head_dims(gpu, bs, d):
-    print(f"case prefill bs={bs} d={d}", flush=True)
-    _check(_make_case([200, 77, 31, 513], [200, 40, 31, 100], 8, 2, d, bs, torch.bfloat16, seed=bs + d),
-           f"bs={bs} d={d}", sm_scale=0.1)
+@pytest.mark.parametrize("long_q", [False, True])
+def test_prefill_block_sizes_and_head_dims(gpu, bs, d, long_q):
+    print(f"case prefill bs={bs} d={d} long_q={long_q}", flush=True)
+    lens_k, lens_q = ([900, 77, 31, 1100], [600, 40, 31, 513]) if long_q else ([200, 77, 31, 513], [200, 40, 31, 100])
+    _check(_make_case(lens_k, lens_q, 8, 2, d, bs, torch.bfloat16, seed=bs + d + (1 if long_q else 0)),
+           f"bs={bs} d={d} long_q={long_q}", sm_scale=0.1)
 
 
-def test_prefill_matches_packed_varlen_bitwise(gpu):
+@pytest.mark.parametrize("long_q", [False, True])
+def test_prefill_matches_packed_varlen_bitwise(gpu, long_q):
     """With the cache holding the packed K/V in order, the paged and packed
-    forwards fill identical LDS tiles: outputs and lse agree bit for bit."""
-    print("case prefill vs packed varlen", flush=True)
+    forwards fill identical LDS tiles: outputs and lse agree bit for bit
+    (with runs of 512 queries or more both take 8-wave workgroups)."""
+    print(f"case prefill vs packed varlen long_q={long_q}", flush=True)
     lens_k, lens_q, hq, hkv, d, bs = [700, 64, 257, 1], [300, 64, 1, 1], 16, 4, 128, 16
+    if long_q:
+        lens_k, lens_q = [1500, 64, 700, 1], [700, 64, 513, 1]
     q, kc, vc, table, cu, sl = _make_case(lens_k, lens_q, hq, hkv, d, bs, torch.bfloat16, seed=5)
     k_packed = torch.cat([kc[table[b, :(n + bs - 1) // bs].long()].reshape(-1, hkv, d)[:n]
                           for b, n in enumerate(lens_k)])
