@@ -12,7 +12,7 @@
 // a dq workspace, :323-325, followed by a cast, :382), the work is split into
 // two kernels; by default
 //   fa_bwd_dq_kernel   : query-stationary. Its prologue does the reference's
-//                        preprocess (:341-350): delta and L*log2(e) per query
+//                        preprocess (:341-350): L*log2(e) and -delta per query
 //                        row into the workspace. Then dQ = scale * dS K over
 //                        all visible key tiles, stored straight in the input
 //                        dtype;
@@ -24,6 +24,8 @@
 //   fa_bwd_dq_ds_kernel : dQ = scale * dS K over the stored dS,
 // which computes S and dP once but moves dS through HBM twice.
 // There are no atomics and no fp32 dq buffer, so results are deterministic.
+// Every dP accumulation starts from -delta (the MFMA's C input), so that
+// dS = P (dP - delta) costs one multiply per score.
 #include "fa_common.hpp"
 
 namespace lsfa {
@@ -144,11 +146,15 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   const float delta = half_sum(dpart);
   const float l2 = lraw == -INFINITY ? INFINITY : lraw * kLog2eB;  // no visible key / padding: P == 0
   if (hh == 0) {
-    float2 v;
-    v.x = l2;
-    v.y = delta;
-    *(float2*)(p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 2 * (int64_t)qrow) = v;
+    float* w = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + (qrow >> 6) * 128 + (qrow & 63);
+    w[0] = l2;
+    w[64] = -delta;
   }
+  // dP^T - delta accumulates from -delta (this lane's query in every
+  // register), so dS = P (dP - delta) is one multiply per score.
+  f32x16 negd;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) negd[i] = -delta;
   __syncthreads();  // the K/V tiles below reuse the Q/dO buffers
 
   int kv_end = nk;
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         s[kb] = f32x16{};
-        dp[kb] = f32x16{};
+        dp[kb] = negd;
       }
 #pragma unroll
       for (int kk = 0; kk < KSTEPS; ++kk) {
@@ -214,10 +220,11 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
           dp[kb] = mfma32(*(const LDS_AS X8*)(Vs + o), doreg[kk], dp[kb]);
         }
       }
-      // K / V operand reads run 8 MFMAs ahead of their MFMA (the compiler's
-      // order reads one ahead and waits out an LDS latency per MFMA).
+      // K / V operand reads run 4 MFMAs ahead of their MFMA (the compiler's
+      // order reads one ahead and waits out an LDS latency per MFMA; eight
+      // ahead no longer fits beside the -delta block).
       {
-        constexpr int NM = 2 * KSTEPS * KB, RA = 8;
+        constexpr int NM = 2 * KSTEPS * KB, RA = 4;
 #pragma unroll
         for (int i = 0; i < RA; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
@@ -231,7 +238,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const float pv = fast_exp2(fmaf(s[kb][i], sl2, -l2));
-          s[kb][i] = pv * (dp[kb][i] - delta);
+          s[kb][i] = pv * dp[kb][i];
         }
       if (CAUSAL && kbase + BN - 1 > qw_lo + off) {  // tile crosses the diagonal
         const int lim = qrow + off - kbase - 4 * hh;  // masked if 32kb + 8(i/4) + i%4 > lim
@@ -289,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 // dK, dV. Workgroup = 4 waves, one per SIMD, over 128 keys; wave w owns keys
 // 32w..32w+31 and keeps their K and V rows in registers for the whole kernel
 // (the B operands of S = Q K^T and dP = dO V^T). Q, dO and the rows'
-// (L*log2e, delta) pairs stream through three LDS stages of 64-row tiles by
+// L*log2e and -delta blocks stream through three LDS stages of 64-row tiles by
 // direct buffer loads. Each wave walks the 32-row halves of the tiles in
 // order, software-pipelined so that its own MFMA and VALU work overlap (a
 // wave's MFMAs run beside its own independent VALU instructions, not beside
@@ -321,7 +328,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   constexpr int NW = 4, BNK = 128, BMQ = 64, NST = 3;
   constexpr int KSTEPS = DP / 16, DT = DP / 32;
   constexpr int R_B = BMQ * DP * 2;     // bytes of a row-major Q (or dO) tile
-  constexpr int RS_B = 2 * R_B + 1024;  // one stage: Q | dO | (L*log2e, delta) pairs, 1 KB aligned
+  constexpr int RS_B = 2 * R_B + 1024;  // one stage: Q | dO | 64 L*log2e | 64 -delta, 1 KB aligned
   constexpr int LDS_B = NST * RS_B;
   constexpr int CR = 2 * R_B / 1024 / NW;  // 1 KB chunks per wave per tile (Q|dO)
   static_assert(CR >= 1, "tile too small for the workgroup");
@@ -464,19 +471,32 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   // chunk; phase Y has NCY = 4 DT chunks, the first 2 DT of them (step ks = 0)
   // carrying the 8 conversions of P1 / G1 that the rest need.
   constexpr int NCX = 2 * KSTEPS, EPC = 16 / NCX, NCY = 4 * DT, CPY = 8 / (2 * DT);
+  // -delta of the 16 queries a lane's score registers hold in half q of the
+  // tile in stage st (register i: query 32 q + 8 (i / 4) + 4 hh + i % 4),
+  // the start of its dP - delta accumulation: four 16-byte reads.
+  auto neg_delta = [&](const LDS_AS char* st, int q) -> f32x16 {
+    const LDS_AS f32x4* d = (const LDS_AS f32x4*)(st + 2 * R_B + 256 + (32 * q + 4 * hh) * 4);
+    f32x16 r;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 v = d[2 * g];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[4 * g + e] = v[e];
+    }
+    return r;
+  };
   auto phase_x = [&](const LDS_AS char* nst, int nq, f32x16& sn, f32x16& dn, const LDS_AS char* stg, int t, int q,
                      f32x16& s, f32x16& dp) {
     const LDS_AS char* an = nst + 32 * nq * DP * 2;
     // operand c: kk = c / 2; even c reads a Q row (S), odd c a dO row (dP)
     auto opread = [&](int c) -> X8 { return *(const LDS_AS X8*)(an + (c & 1) * R_B + roff[c >> 1]); };
-    // (L*log2e, delta) of queries 8g + 4hh .. +3 (group g = scores 4g .. 4g+3,
-    // 8-byte pairs at byte 64 g): two 16-byte reads, issued four chunks
-    // before the group's first score is scaled.
-    const LDS_AS f32x4* ldp = (const LDS_AS f32x4*)(stg + 2 * R_B + (32 * q + 4 * hh) * 8);
-    f32x4 lda[4], ldc[4];
+    // L*log2e of queries 8g + 4hh .. +3 (group g = scores 4g .. 4g+3): one
+    // 16-byte read, issued four chunks before the group's first score is
+    // scaled.
+    const LDS_AS f32x4* ldp = (const LDS_AS f32x4*)(stg + 2 * R_B + (32 * q + 4 * hh) * 4);
+    f32x4 lda[4];
     auto lead = [](int g) { return 4 * g / EPC - 4; };
-    auto l2_of = [&](int i) { const int g = i >> 2, e = i & 3; return e < 2 ? lda[g][2 * e] : ldc[g][2 * (e - 2)]; };
-    auto dl_of = [&](int i) { const int g = i >> 2, e = i & 3; return e < 2 ? lda[g][2 * e + 1] : ldc[g][2 * (e - 2) + 1]; };
+    auto l2_of = [&](int i) { return lda[i >> 2][i & 3]; };
     // Each score goes through three steps two chunks apart (x = s*scale*log2e
     // - L*log2e; p = exp2(x); dS = p (dP - delta)), so the VALU instructions
     // of one chunk never wait on each other.
@@ -492,19 +512,16 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     };
     auto step_c = [&](int cc) {
 #pragma unroll
-      for (int u = 0; u < EPC; ++u) { const int i = cc * EPC + u; dp[i] = s[i] * (dp[i] - dl_of(i)); }
+      for (int u = 0; u < EPC; ++u) { const int i = cc * EPC + u; dp[i] = s[i] * dp[i]; }
     };
     X8 op[PF + 1];
 #pragma unroll
     for (int c = 0; c < PF && c < NCX; ++c) op[c] = opread(c);
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      if (lead(g) < 0) {
-        lda[g] = ldp[4 * g];
-        ldc[g] = ldp[4 * g + 1];
-      }
+      if (lead(g) < 0) lda[g] = ldp[2 * g];
     sn = f32x16{};
-    dn = f32x16{};
+    dn = neg_delta(nst, nq);
     step_a(0);
     step_a(1);
     step_b(0);
@@ -514,10 +531,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
       if (c + PF < NCX) op[(c + PF) % (PF + 1)] = opread(c + PF);
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        if (lead(g) == c) {
-          lda[g] = ldp[4 * g];
-          ldc[g] = ldp[4 * g + 1];
-        }
+        if (lead(g) == c) lda[g] = ldp[2 * g];
       if (c & 1)
         dn = mfma32(op[c % (PF + 1)], vreg[c >> 1], dn);
       else
@@ -598,7 +612,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   auto scores = [&](const LDS_AS char* stg, int q, f32x16& s, f32x16& dp) {
     const LDS_AS char* st = stg + 32 * q * DP * 2;
     s = f32x16{};
-    dp = f32x16{};
+    dp = neg_delta(stg, q);
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
       s = mfma32(*(const LDS_AS X8*)(st + roff[kk]), kreg[kk], s);
@@ -659,8 +673,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
 // ---------------------------------------------------------------------------
 // Preprocess of the stored-dS path (kernels/flash_attention_backward.py:
 // 341-350): per query row delta = rowsum(dO * O) (products of the input-dtype
-// values in fp32) and L * log2(e) into the ld workspace; rows Nq .. nq_pad-1
-// and rows whose L is -inf get (+inf, 0), so that their P is exactly 0.
+// values in fp32) and L * log2(e) into the ld workspace (L * log2(e) and
+// -delta); rows Nq .. nq_pad-1 and rows whose L is -inf get (+inf, 0), so
+// that their P is exactly 0.
 // Block = 64 rows x 4 lanes; lane part of a row sums the 16-byte chunks
 // part, part + 4, ... of both rows.
 // ---------------------------------------------------------------------------
@@ -693,10 +708,9 @@ __global__ __launch_bounds__(256) void fa_bwd_prep_kernel(const BwdParams p) {
   acc += __shfl_xor(acc, 1);
   acc += __shfl_xor(acc, 2);
   if (part == 0) {
-    float2 v;
-    v.x = l2;
-    v.y = acc;
-    *(float2*)(p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + 2 * (int64_t)row) = v;
+    float* w = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + (row >> 6) * 128 + (row & 63);
+    w[0] = l2;
+    w[64] = -acc;
   }
 }
 
@@ -929,7 +943,7 @@ static hipError_t launch_bwd_ds(BwdParams p, int phases, hipStream_t s) {
 
 // phases: bit 0 dQ, bit 1 dK/dV. With p.ds set, the stored-dS path above;
 // otherwise the recompute path: fa_bwd_dq_kernel (whose prologue writes the
-// ld pairs), then fa_bwd_dkdv_kernel.
+// ld blocks), then fa_bwd_dkdv_kernel.
 template <typename T, int DP, bool CAUSAL>
 static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
   if (p.ds != nullptr) {

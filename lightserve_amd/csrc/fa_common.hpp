@@ -175,8 +175,11 @@ struct BwdParams {
   void* dk;
   void* dv;
   // Workspace written by the dq kernel's prologue:
-  //   ld  : (lse * log2(e), delta) pairs, element (b, h, q) at b*sldb + h*sldh + 2q;
-  //         +inf stands in for lse where a row sees no key or q >= Nq
+  //   ld  : per (b, h) at b*sldb + h*sldh, blocks of 64 queries: 64 values of
+  //         lse * log2(e), then 64 of -delta (query q's at 128 (q / 64) + q % 64
+  //         and 64 further); +inf stands in for lse where a row sees no key or
+  //         q >= Nq. The fp32 kernels keep (lse * log2(e), delta) pairs, query
+  //         q's at 2q.
   float* ld;
   int64_t sldb, sldh;
   int nq_pad;  // Nq rounded up to the query-stationary tile (128)
