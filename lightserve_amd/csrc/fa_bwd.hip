@@ -440,6 +440,22 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     troff[dt][1] = swz_off<DP>(tr_row + 8, 32 * dt + tr_col) * 2;
   }
 
+  // Lane offsets for the third stage, whose addresses pass the 16-bit
+  // immediate: the same offsets plus 64 KB (kept opaque so that they stay in
+  // registers instead of being re-added per read).
+  int roffH[KSTEPS], troffH[DT][2];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    roffH[kk] = roff[kk] + 65536;
+    asm volatile("" : "+v"(roffH[kk]));
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int j2 = 0; j2 < 2; ++j2) {
+      troffH[dt][j2] = troff[dt][j2] + 65536;
+      asm volatile("" : "+v"(troffH[dt][j2]));
+    }
   f32x16 dk[DT], dv[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
@@ -485,11 +501,13 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     }
     return r;
   };
-  auto phase_x = [&](const LDS_AS char* nst, int nq, f32x16& sn, f32x16& dn, const LDS_AS char* stg, int t, int q,
+  auto phase_x = [&](const LDS_AS char* nst, bool nhi, int nq, f32x16& sn, f32x16& dn, const LDS_AS char* stg, int t, int q,
                      f32x16& s, f32x16& dp) {
     const LDS_AS char* an = nst + 32 * nq * DP * 2;
     // operand c: kk = c / 2; even c reads a Q row (S), odd c a dO row (dP)
-    auto opread = [&](int c) -> X8 { return *(const LDS_AS X8*)(an + (c & 1) * R_B + roff[c >> 1]); };
+    auto opread = [&](int c) -> X8 {
+      return *(const LDS_AS X8*)((nhi ? an - 65536 : an) + (c & 1) * R_B + (nhi ? roffH[c >> 1] : roff[c >> 1]));
+    };
     // L*log2e of queries 8g + 4hh .. +3 (group g = scores 4g .. 4g+3): one
     // 16-byte read, issued four chunks before the group's first score is
     // scaled.
@@ -571,14 +589,15 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     G0 = __builtin_bit_cast(X8, g0w);
     store_ds(q0, g0w, 0);
   };
-  auto phase_y = [&](const LDS_AS char* stg, int t, int q, const f32x16& s, const f32x16& dp) {
+  auto phase_y = [&](const LDS_AS char* stg, bool chi, int t, int q, const f32x16& s, const f32x16& dp) {
     const LDS_AS char* st = stg + 32 * q * DP * 2;
     // MFMA c: ks = c / (2 DT), dt = (c / 2) % DT; even c is dV (dO^T), odd c dK (Q^T)
     auto opread = [&](int c) -> X8 {
       const LDS_AS char* qb = st + 16 * (c / (2 * DT)) * DP * 2 + ((c & 1) ? 0 : R_B);
       const int dt = (c >> 1) % DT;
-      return cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(qb + troff[dt][0])),
-                          lds_read_tr((const LDS_AS T*)(qb + troff[dt][1])));
+      const LDS_AS char* qh = chi ? qb - 65536 : qb;
+      return cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(qh + (chi ? troffH[dt][0] : troff[dt][0]))),
+                          lds_read_tr((const LDS_AS T*)(qh + (chi ? troffH[dt][1] : troff[dt][1]))));
     };
     X8 op[PF + 1];
 #pragma unroll
@@ -637,10 +656,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
       if (t >= n_t) break;
       const LDS_AS char* stg = sm + si * RS_B;
       const LDS_AS char* nstg = sm + ((si + 1) % NST) * RS_B;
-      phase_x(stg, 1, sb, db, stg, t, 0, sa, da);
-      phase_y(stg, t, 0, sa, da);
-      phase_x(nstg, 0, sa, da, stg, t, 1, sb, db);
-      phase_y(stg, t, 1, sb, db);
+      const bool chi = si == 2, nhi = (si + 1) % NST == 2;
+      phase_x(stg, chi, 1, sb, db, stg, t, 0, sa, da);
+      phase_y(stg, chi, t, 0, sa, da);
+      phase_x(nstg, nhi, 0, sa, da, stg, t, 1, sb, db);
+      phase_y(stg, chi, t, 1, sb, db);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (t + NST < n_t) load_tile(t_begin + t + NST, si, rvo);
