@@ -89,7 +89,8 @@ typedef struct {
  * least lsfa_bwd_workspace_size() bytes, 256-byte aligned; its contents on
  * entry do not matter and are scratch afterwards. It receives what the
  * reference's preprocess kernel computes (delta = rowsum(dO * O),
- * kernels/flash_attention_backward.py:202-229) with L*log2(e) per query row.
+ * kernels/flash_attention_backward.py:202-229, stored negated) with
+ * L*log2(e) per query row.
  * By default a query-stationary kernel produces dq and a key-stationary one
  * dk and dv, each computing S and dP itself. With LSFA_BWD_STORED_DS (bf16 /
  * fp16 at head_dim above 64) the key-stationary kernel also stores dS (in
