@@ -238,14 +238,17 @@ def test_graph_capture_and_side_stream(gpu):
         _ = (q.float() * 2).sum().item()  # unrelated eager work between replays
 
 
-@pytest.mark.parametrize("B,H,N,D,causal", [(1, 5, 4100, 128, True), (1, 3, 4352, 64, False), (2, 2, 4097, 64, True)])
-def test_wide_workgroups(gpu, B, H, N, D, causal):
+@pytest.mark.parametrize("B,H,N,D,causal,dtype", [(1, 5, 4100, 128, True, torch.bfloat16),
+                                                   (1, 3, 4352, 64, False, torch.bfloat16),
+                                                   (2, 2, 4097, 64, True, torch.bfloat16),
+                                                   (1, 3, 4160, 128, True, torch.float16)])
+def test_wide_workgroups(gpu, B, H, N, D, causal, dtype):
     """Dense launches of at least 4096 queries (head dim >= 64) run 8-wave,
     256-row workgroups: sequence ends that are not a multiple of 256 (or of
     the 64-key tile), every (b, h) slice against the oracle."""
-    print(f"case wide forward {B}x{H}x{N}x{D} causal={causal}", flush=True)
+    print(f"case wide forward {B}x{H}x{N}x{D} causal={causal} {dtype}", flush=True)
     g = torch.Generator().manual_seed(N + D)
-    q, k, v = (torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).to(gpu) for _ in range(3))
+    q, k, v = (torch.randn(B, H, N, D, generator=g).to(dtype).to(gpu) for _ in range(3))
     o, lse = flash_attention_forward(q, k, v, causal=causal, return_lse=True)
     o_ref, lse_ref = _oracle_gpu_chunked(q.float(), k.float(), v.float(), causal, heads_per_chunk=1)
     assert_gate(o.float(), o_ref, f"wide {N} o")

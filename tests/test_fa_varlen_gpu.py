@@ -86,12 +86,18 @@ def _varlen_poisoned(q, k, v, cu_q, cu_k, max_q, max_k, causal):
     return o, lse
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,causal,long_q", [(64, 8, 2, True, False), (65, 8, 2, True, False),
-                                                     (40, 6, 3, False, False), (23, 16, 4, True, False),
-                                                     (1, 24, 8, True, False), (64, 8, 2, True, True),
-                                                     (65, 8, 2, True, True), (23, 16, 4, True, True),
-                                                     (40, 6, 3, False, True)])
-def test_varlen_every_item_once(gpu, B, Hq, Hkv, causal, long_q):
+@pytest.mark.parametrize("B,Hq,Hkv,causal,long_q,dtype", [(64, 8, 2, True, False, torch.bfloat16),
+                                                           (65, 8, 2, True, False, torch.bfloat16),
+                                                           (40, 6, 3, False, False, torch.bfloat16),
+                                                           (23, 16, 4, True, False, torch.bfloat16),
+                                                           (1, 24, 8, True, False, torch.bfloat16),
+                                                           (64, 8, 2, True, True, torch.bfloat16),
+                                                           (65, 8, 2, True, True, torch.bfloat16),
+                                                           (23, 16, 4, True, True, torch.bfloat16),
+                                                           (40, 6, 3, False, True, torch.bfloat16),
+                                                           (23, 16, 4, True, True, torch.float16),
+                                                           (40, 6, 3, False, True, torch.float16)])
+def test_varlen_every_item_once(gpu, B, Hq, Hkv, causal, long_q, dtype):
     """Batches of up to 64 sequences take their (sequence, query tile) items
     longest-first, found per workgroup from cu_seqlens; longer batches keep
     the head-major order. Lengths mix empty chunks, chunks longer than their
@@ -100,7 +106,7 @@ def test_varlen_every_item_once(gpu, B, Hq, Hkv, causal, long_q):
     sequences take 256-row tiles (8-wave workgroups), so the lengths also
     straddle 256-row edges. Every output row must be written once and match
     the oracle."""
-    print(f"case varlen order B={B} Hq={Hq} Hkv={Hkv} causal={causal} long_q={long_q}", flush=True)
+    print(f"case varlen order B={B} Hq={Hq} Hkv={Hkv} causal={causal} long_q={long_q} {dtype}", flush=True)
     g = torch.Generator().manual_seed(B * 100 + Hq + (7 if long_q else 0))
     choices_q = [0, 1, 64, 127, 128, 129, 200, 256, 300]
     if long_q:
@@ -114,9 +120,9 @@ def test_varlen_every_item_once(gpu, B, Hq, Hkv, causal, long_q):
     cu_q = torch.tensor([0] + torch.tensor(lens_q).cumsum(0).tolist(), dtype=torch.int32)
     cu_k = torch.tensor([0] + torch.tensor(lens_k).cumsum(0).tolist(), dtype=torch.int32)
     D = 64
-    q = torch.randn(int(cu_q[-1]), Hq, D, generator=g).to(torch.bfloat16)
-    k = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).to(torch.bfloat16)
-    v = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(int(cu_q[-1]), Hq, D, generator=g).to(dtype)
+    k = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).to(dtype)
+    v = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).to(dtype)
     o, lse = _varlen_poisoned(q.to(gpu), k.to(gpu), v.to(gpu), cu_q.to(gpu), cu_k.to(gpu),
                               max(lens_q), max(lens_k), causal)
     assert not torch.isnan(o).any(), "output rows left unwritten"
