@@ -175,18 +175,28 @@ __global__ __launch_bounds__(256) void fa_decode_split_kernel(const DecodeParams
         m[g] = mx;
       }
     }
+    // P V two tokens at a time on v_dot2 (each pair of V rows interleaved by
+    // v_perm_b32, shared by the G heads), with p rounded to the input dtype
+    // as the forward's PV operands are. The row sums stay fp32: the offset
+    // is the exact running max, so the largest p is 1 and exact, and the
+    // rounding moves O by at most ~2^-9 of |v| while L keeps fp32 accuracy.
+    typedef __attribute__((ext_vector_type(2))) T T2;
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const X8 vv = __builtin_bit_cast(X8, vr[u]);
-      float vf[8];
+    for (int u = 0; u < CH; u += 2) {
+      T2 vp[8];  // (token u, token u+1) of dim e
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vf[e] = (float)vv[e];
+      for (int j = 0; j < 4; ++j) {
+        vp[2 * j] = __builtin_bit_cast(T2, __builtin_amdgcn_perm(vr[u + 1][j], vr[u][j], 0x05040100u));
+        vp[2 * j + 1] = __builtin_bit_cast(T2, __builtin_amdgcn_perm(vr[u + 1][j], vr[u][j], 0x07060302u));
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float pv = fast_exp2(s[u][g] - m[g]);  // exp2(-inf) = 0 past the end
-        l[g] += pv;
+        const float p0 = fast_exp2(s[u][g] - m[g]);  // exp2(-inf) = 0 past the end
+        const float p1 = fast_exp2(s[u + 1][g] - m[g]);
+        const T2 pp = T2{(T)p0, (T)p1};
+        l[g] += p0 + p1;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv, vf[e], acc[g][e]);
+        for (int e = 0; e < 8; ++e) acc[g][e] = dot2(pp, vp[e], acc[g][e]);
       }
     }
   };
