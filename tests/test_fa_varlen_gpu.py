@@ -130,3 +130,45 @@ def test_varlen_every_item_once(gpu, B, Hq, Hkv, causal, long_q, dtype):
     o_ref, lse_ref = varlen_reference(q, k, v, cu_q, cu_k, causal=causal)
     assert_gate(o.cpu(), o_ref, f"varlen order B={B}")
     assert_lse(lse.cpu(), lse_ref, f"varlen order B={B}")
+
+
+def test_varlen_random_batches(gpu):
+    """Seeded random batches through both launch shapes (4-wave and, with runs
+    of 512 queries or more, 8-wave workgroups) and both orders (up to 64
+    sequences longest-first, more head-major): batch sizes 1-70, ragged and
+    empty chunks, chunks longer than their keys, GQA groups 1-8, head dims
+    64/96/128, bf16/fp16, causal or not. Every row must be written once
+    (NaN-poisoned outputs) and match the oracle."""
+    rng = torch.Generator().manual_seed(2024)
+    ri = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=rng))
+    for case in range(24):
+        # modes bound the fp64 oracle's work: few long runs (8-wave), many
+        # short sequences (past the 64-sequence limit), or in between
+        mode = case % 3
+        B = ri(1, 6) if mode == 0 else (ri(40, 70) if mode == 1 else ri(1, 20))
+        qmax, kextra = (900, 700) if mode == 0 else ((100, 150) if mode == 1 else (300, 400))
+        Hkv = [1, 2, 4][ri(0, 2)]
+        G = [1, 2, 3, 4, 8][ri(0, 4)]
+        D = [64, 96, 128][ri(0, 2)]
+        dtype = [torch.bfloat16, torch.float16][ri(0, 1)]
+        causal = bool(ri(0, 1))
+        lens_q = torch.randint(0, qmax + 1, (B,), generator=rng).tolist()
+        if mode == 0:
+            lens_q[0] = max(lens_q[0], 512)
+        lens_k = [max(0, lq + int(d)) for lq, d in zip(lens_q, torch.randint(-qmax // 8, kextra, (B,), generator=rng))]
+        print(f"case varlen random {case}: B={B} Hq={Hkv * G} Hkv={Hkv} D={D} {dtype} causal={causal} "
+              f"max_q={max(lens_q)}", flush=True)
+        cu_q = torch.tensor([0] + torch.tensor(lens_q).cumsum(0).tolist(), dtype=torch.int32)
+        cu_k = torch.tensor([0] + torch.tensor(lens_k).cumsum(0).tolist(), dtype=torch.int32)
+        if int(cu_q[-1]) == 0:
+            continue
+        q = torch.randn(int(cu_q[-1]), Hkv * G, D, generator=rng).to(dtype)
+        k = torch.randn(max(int(cu_k[-1]), 1), Hkv, D, generator=rng).to(dtype)
+        v = torch.randn(max(int(cu_k[-1]), 1), Hkv, D, generator=rng).to(dtype)
+        o, lse = _varlen_poisoned(q.to(gpu), k.to(gpu), v.to(gpu), cu_q.to(gpu), cu_k.to(gpu),
+                                  max(lens_q), max(max(lens_k), 1), causal)
+        assert not torch.isnan(o).any(), f"case {case}: output rows left unwritten"
+        assert not torch.isnan(lse).any(), f"case {case}: lse rows left unwritten"
+        o_ref, lse_ref = varlen_reference(q, k, v, cu_q, cu_k, causal=causal)
+        assert_gate(o.cpu(), o_ref, f"varlen random {case}")
+        assert_lse(lse.cpu(), lse_ref, f"varlen random {case}")
