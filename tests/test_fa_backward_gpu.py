@@ -15,7 +15,7 @@ from lightserve_amd.kernels.flash_attention_backward import (_flash_attention_ba
                                                              flash_attention)
 from oracle.attention import attention_grads, attention_reference, flash_backward_tiled
 from lightserve_amd.workloads import make_config_inputs
-from tests.gates import assert_gate, assert_grad_parity
+from tests.gates import assert_gate, assert_grad_parity, assert_lse
 
 pytestmark = pytest.mark.gpu
 
@@ -226,3 +226,39 @@ def test_stored_ds_matches_default(gpu, B, H, Nq, Nk, causal):
         err = (a.float() - b.float()).abs()
         scale = b.float().abs().max().item()
         assert err.max().item() <= 1e-2 * scale and err.mean().item() <= 1e-3 * scale, (name, err.max().item(), scale)
+
+def _random_case(seed):
+    import random
+    r = random.Random(seed)
+    B, H = r.randint(1, 3), r.randint(1, 4)
+    Nq = r.choice([r.randint(1, 80), r.randint(60, 700), r.randint(500, 1200)])
+    Nk = Nq if r.random() < 0.5 else r.randint(1, 1200)
+    D = r.choice([16, 32, 64, 80, 96, 128])
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    return B, H, Nq, Nk, D, dtype, r.random() < 0.5
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_fwd_bwd(gpu, seed):
+    """Seeded random shapes (ragged lengths on both sides, Nq != Nk, head dims
+    that need padding, bf16/fp16, causal or not) through the C ABI, with the
+    backward workspace starting as NaN bytes: o and L against the oracle's
+    forward, dQ/dK/dV against its float64 autograd under the gradient gate."""
+    B, H, Nq, Nk, D, dtype, causal = _random_case(seed)
+    print(f"case random bwd seed={seed} {B}x{H} Nq={Nq} Nk={Nk} D={D} {dtype} causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(1000 + seed)
+    q, do = (torch.randn(B, H, Nq, D, generator=g).to(dtype) for _ in range(2))
+    k, v = (torch.randn(B, H, Nk, D, generator=g).to(dtype) for _ in range(2))
+    scale = D ** -0.5
+    o, L, dq, dk, dv = _abi_fwd_bwd(*(t.to(gpu) for t in (q, k, v, do)), causal, scale, poison=True)
+    torch.cuda.synchronize()
+    o_ref, l_ref = attention_reference(q, k, v, causal, scale)
+    assert_lse(L.cpu(), l_ref, f"seed {seed} L")
+    seen = torch.isfinite(l_ref)
+    assert torch.equal(o.cpu()[~seen], torch.zeros_like(o.cpu()[~seen])), "rows that see no key must give o = 0"
+    assert_gate(o.cpu().double()[seen], o_ref[seen], f"seed {seed} o")
+    exact = attention_grads(q, k, v, do, causal, scale)
+    ref_alg = flash_backward_tiled(q, k, v, o_ref.nan_to_num().to(dtype), l_ref, do, causal, scale,
+                                   op_dtype=dtype)
+    for name, got, ex, ra in zip(("dq", "dk", "dv"), (dq, dk, dv), exact, ref_alg):
+        assert_grad_parity(got.cpu(), ex.nan_to_num(), ra.nan_to_num(), f"seed {seed} {name}")
