@@ -238,14 +238,11 @@ def _random_case(seed):
     return B, H, Nq, Nk, D, dtype, r.random() < 0.5
 
 
-@pytest.mark.parametrize("seed", range(24))
-def test_random_fwd_bwd(gpu, seed):
-    """Seeded random shapes (ragged lengths on both sides, Nq != Nk, head dims
-    that need padding, bf16/fp16, causal or not) through the C ABI, with the
-    backward workspace starting as NaN bytes: o and L against the oracle's
-    forward, dQ/dK/dV against its float64 autograd under the gradient gate."""
-    B, H, Nq, Nk, D, dtype, causal = _random_case(seed)
-    print(f"case random bwd seed={seed} {B}x{H} Nq={Nq} Nk={Nk} D={D} {dtype} causal={causal}", flush=True)
+def _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, seed, what):
+    """Forward with L and backward through the C ABI (workspace poisoned with
+    NaN bytes) against the oracle: L and o under the forward gate (rows that
+    see no key: L = -inf, o = 0), dQ/dK/dV against the float64 autograd under
+    the gradient gate."""
     g = torch.Generator().manual_seed(1000 + seed)
     q, do = (torch.randn(B, H, Nq, D, generator=g).to(dtype) for _ in range(2))
     k, v = (torch.randn(B, H, Nk, D, generator=g).to(dtype) for _ in range(2))
@@ -253,12 +250,31 @@ def test_random_fwd_bwd(gpu, seed):
     o, L, dq, dk, dv = _abi_fwd_bwd(*(t.to(gpu) for t in (q, k, v, do)), causal, scale, poison=True)
     torch.cuda.synchronize()
     o_ref, l_ref = attention_reference(q, k, v, causal, scale)
-    assert_lse(L.cpu(), l_ref, f"seed {seed} L")
+    assert_lse(L.cpu(), l_ref, f"{what} L")
     seen = torch.isfinite(l_ref)
     assert torch.equal(o.cpu()[~seen], torch.zeros_like(o.cpu()[~seen])), "rows that see no key must give o = 0"
-    assert_gate(o.cpu().double()[seen], o_ref[seen], f"seed {seed} o")
+    assert_gate(o.cpu().double()[seen], o_ref[seen], f"{what} o")
     exact = attention_grads(q, k, v, do, causal, scale)
     ref_alg = flash_backward_tiled(q, k, v, o_ref.nan_to_num().to(dtype), l_ref, do, causal, scale,
                                    op_dtype=dtype)
     for name, got, ex, ra in zip(("dq", "dk", "dv"), (dq, dk, dv), exact, ref_alg):
-        assert_grad_parity(got.cpu(), ex.nan_to_num(), ra.nan_to_num(), f"seed {seed} {name}")
+        assert_grad_parity(got.cpu(), ex.nan_to_num(), ra.nan_to_num(), f"{what} {name}")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_fwd_bwd(gpu, seed):
+    """Seeded random shapes (ragged lengths on both sides, Nq != Nk, head dims
+    that need padding, bf16/fp16, causal or not) through the C ABI."""
+    B, H, Nq, Nk, D, dtype, causal = _random_case(seed)
+    print(f"case random bwd seed={seed} {B}x{H} Nq={Nq} Nk={Nk} D={D} {dtype} causal={causal}", flush=True)
+    _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, seed, f"seed {seed}")
+
+
+@pytest.mark.parametrize("Nq,Nk,causal,dtype", [(4160, 4160, True, torch.bfloat16), (4100, 700, True, torch.float16),
+                                                (4097, 5000, False, torch.bfloat16), (4352, 4352, False, torch.float16)])
+def test_long_query_dq_workgroups(gpu, Nq, Nk, causal, dtype):
+    """From 4096 queries at head dim 128 the dQ kernel runs 256-row (8-wave)
+    workgroups; ragged ends (a last tile past the workspace's 128-row
+    padding), rows that see no key and Nq != Nk on that path."""
+    print(f"case long-q dq Nq={Nq} Nk={Nk} causal={causal} {dtype}", flush=True)
+    _check_fwd_bwd(gpu, 1, 2, Nq, Nk, 128, dtype, causal, Nq + Nk, f"long-q {Nq}x{Nk}")
