@@ -35,24 +35,20 @@ constexpr float kLog2eB = 1.4426950408889634f;
 constexpr int kCacheNT = 2;
 
 // ---------------------------------------------------------------------------
-// dQ. Workgroup = NW waves x 32 query rows, at most 256 registers per wave:
-// 4 waves (two workgroups per CU; Q and dO reach the registers through LDS)
-// or, for long sequences at head dim 128, 8 waves (one workgroup per CU; Q
-// and dO are read straight into the registers, each K/V tile serves 256
-// rows). K/V tiles of 64 keys go global -> LDS with buffer_load ... lds
-// (double-buffered, zero past the sequence end).
+// dQ. Workgroup = 4 waves x 32 query rows, at most 256 registers
+// per wave so two workgroups share a CU. K/V tiles of 64 keys go global ->
+// LDS with buffer_load ... lds (double-buffered, zero past the sequence end).
 // Per key tile and wave:
 //   S^T  = K Q^T          A = K rows (LDS),  B = Q^T  (registers)
 //   dP^T = V dO^T         A = V rows (LDS),  B = dO^T (registers)
 //   dS^T = P^T (dP^T - delta)  -> rounded into B operands
 //   dQ^T += K^T dS^T      A = K^T via transpose reads of the same LDS tile
 // ---------------------------------------------------------------------------
-template <typename T, int DP, bool CAUSAL, int NW>
-__global__ __launch_bounds__(NW * 64, 8 / NW) void fa_bwd_dq_kernel(const BwdParams p) {
+template <typename T, int DP, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
-  static_assert(NW == 4 || NW == 8, "4 waves (two workgroups per CU) or 8 (one)");
-  constexpr int BM = NW * 32, BN = 64;
+  constexpr int NW = 4, BM = NW * 32, BN = 64;
   constexpr int TILE = BN * DP;
   constexpr int LDI = TILE * 2 / 1024 / NW;
   constexpr int KSTEPS = DP / 16;
@@ -109,9 +105,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fa_bwd_dq_kernel(const BwdPar
   //   - Q^T and dO^T B operands of this kernel come from LDS;
   //   - delta = rowsum(dO * O) and L*log2e are written to the workspace for
   //     the dK/dV kernel.
-  constexpr int TB = BM * DP * 2;  // bytes of one BM-row tile
-  constexpr bool QLDS = 2 * TB <= 4 * TILE * 2;  // Q/dO tiles fit in the K/V buffers (4 waves)
-  if constexpr (QLDS) {
+  constexpr int TB = BM * DP * 2;  // bytes of one 128-row tile
+  static_assert(2 * TB <= 4 * TILE * 2, "Q/dO tiles must fit in the K/V buffers");
+  {
     constexpr int CPW = 2 * TB / 1024 / NW;  // chunks per wave (waves 0..1: Q, 2..3: dO)
     const bool w_do = wave >= NW / 2;
     const int64_t sn = w_do ? p.sdon : p.sqn;
@@ -122,20 +118,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fa_bwd_dq_kernel(const BwdPar
       const int c = wave * CPW + i;
       const int vo = row_voff(c % (TB / 1024), sn);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(sm + c * 1024), 16, vo, 0, 0, 0);
-    }
-  }
-  X8 qreg[KSTEPS], doreg[KSTEPS];
-  if constexpr (!QLDS) {  // 8 waves: the lane's own Q / dO segments straight from global memory
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      const int col = 16 * kk + 8 * hh;
-      u32x4 qa{0, 0, 0, 0}, da{0, 0, 0, 0};
-      if (qvalid && col < D) {
-        qa = ldg16(Q + (int64_t)qrow * p.sqn + col);
-        da = ldg16(dO + (int64_t)qrow * p.sdon + col);
-      }
-      qreg[kk] = __builtin_bit_cast(X8, qa);
-      doreg[kk] = __builtin_bit_cast(X8, da);
     }
   }
   u32x4 oraw[KSTEPS];
@@ -150,21 +132,20 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fa_bwd_dq_kernel(const BwdPar
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
+  X8 qreg[KSTEPS], doreg[KSTEPS];
   float dpart = 0.f;
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
-    if constexpr (QLDS) {
-      const int o = swz_off<DP>(32 * wave + l32, 16 * kk + 8 * hh) * 2;
-      qreg[kk] = *(const LDS_AS X8*)(sm + o);
-      doreg[kk] = *(const LDS_AS X8*)(sm + TB + o);
-    }
+    const int o = swz_off<DP>(32 * wave + l32, 16 * kk + 8 * hh) * 2;
+    qreg[kk] = *(const LDS_AS X8*)(sm + o);
+    doreg[kk] = *(const LDS_AS X8*)(sm + TB + o);
     const X8 ov = __builtin_bit_cast(X8, oraw[kk]);
 #pragma unroll
     for (int s = 0; s < 8; ++s) dpart += (float)doreg[kk][s] * (float)ov[s];
   }
   const float delta = half_sum(dpart);
   const float l2 = lraw == -INFINITY ? INFINITY : lraw * kLog2eB;  // no visible key / padding: P == 0
-  if (hh == 0 && qrow < p.nq_pad) {  // the workspace ends at nq_pad (a 256-row tile may pass it)
+  if (hh == 0) {
     float* w = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + (qrow >> 6) * 128 + (qrow & 63);
     w[0] = l2;
     w[64] = -delta;
@@ -983,10 +964,6 @@ static hipError_t launch_bwd_ds(BwdParams p, int phases, hipStream_t s) {
 // phases: bit 0 dQ, bit 1 dK/dV. With p.ds set, the stored-dS path above;
 // otherwise the recompute path: fa_bwd_dq_kernel (whose prologue writes the
 // ld blocks), then fa_bwd_dkdv_kernel.
-#ifndef DQ8_MIN_NQ
-#define DQ8_MIN_NQ 4096
-#endif
-
 template <typename T, int DP, bool CAUSAL>
 static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
   if (p.ds != nullptr) {
@@ -1000,20 +977,10 @@ static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
   const int BH = p.B * p.H;
   p.bh0 = 0;
   p.nbh = BH;
-  // Long sequences at head dim 128: 8-wave workgroups over 256 queries share
-  // each K/V tile load between twice the rows (-0.3 to -1.1% on the backward
-  // from 4096 queries; slower at 2048 and at head dim 64).
-  const bool w8 = DP == 128 && p.Nq >= DQ8_MIN_NQ;
-  const int bm = w8 ? 256 : 128;
-  p.num_tiles = (p.Nq + bm - 1) / bm;
+  p.num_tiles = (p.Nq + 127) / 128;
   p.heads_per_group = heads_per_group_for((long long)p.Nk * DP * 2 * 2);  // K and V rows of a head
   if ((phases & 1) && p.num_tiles > 0) {
-    if (w8) {
-      if constexpr (DP == 128)
-        hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL, 8>), dim3(p.num_tiles * BH), dim3(512), 0, s, p);
-    } else {
-      hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL, 4>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
-    }
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   p.num_tiles = (p.Nk + 127) / 128;

@@ -272,9 +272,8 @@ def test_random_fwd_bwd(gpu, seed):
 
 @pytest.mark.parametrize("Nq,Nk,causal,dtype", [(4160, 4160, True, torch.bfloat16), (4100, 700, True, torch.float16),
                                                 (4097, 5000, False, torch.bfloat16), (4352, 4352, False, torch.float16)])
-def test_long_query_dq_workgroups(gpu, Nq, Nk, causal, dtype):
-    """From 4096 queries at head dim 128 the dQ kernel runs 256-row (8-wave)
-    workgroups; ragged ends (a last tile past the workspace's 128-row
-    padding), rows that see no key and Nq != Nk on that path."""
+def test_long_query_fwd_bwd(gpu, Nq, Nk, causal, dtype):
+    """Sequences past 4096 queries at head dim 128 (where the forward runs
+    8-wave workgroups): ragged ends, rows that see no key, Nq != Nk."""
     print(f"case long-q dq Nq={Nq} Nk={Nk} causal={causal} {dtype}", flush=True)
     _check_fwd_bwd(gpu, 1, 2, Nq, Nk, 128, dtype, causal, Nq + Nk, f"long-q {Nq}x{Nk}")
