@@ -9,7 +9,8 @@ sizes that are multiples of 16, any group size up to 32) and the lane-group
 kernel (smaller blocks, groups 1/2/4/8). Cases: GQA group sizes 1-32, head
 dims 32-128, block sizes 1/16/32/64, ragged and empty sequences, lengths at
 block and tile boundaries, shuffled physical blocks, split and unsplit
-launches, and the device-side clamp of seq_lens to max_seq_len.
+launches, the device-side clamp of seq_lens to max_seq_len, and 20 seeded
+random batches over all of these.
 """
 import pytest
 import torch
@@ -122,3 +123,27 @@ def test_decode_rejects_bad_arguments(gpu):
     q, kc, vc, table, sl = _make_case([4], 4, 2, 64, 12, torch.bfloat16, gpu, seed=1)
     with pytest.raises(RuntimeError, match="power of two"):
         paged_attention_decode(q.cuda(), kc.cuda(), vc.cuda(), table.cuda(), sl.cuda())
+
+
+def _random_decode_case(seed):
+    import random
+    r = random.Random(seed)
+    hkv = r.choice([1, 2, 4, 8])
+    group = r.choice([1, 2, 4, 8, 3, 6, 12])
+    bs = r.choice([16, 32, 64]) if group not in (1, 2, 4, 8) else r.choice([1, 8, 16, 32, 64])
+    d = r.choice([32, 64, 96, 128])
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    nseq = r.randint(1, 40)
+    lens = [r.choice([0, r.randint(1, 64), r.randint(1, 2000), r.randint(2000, 9000)]) for _ in range(nseq)]
+    return lens, hkv * group, hkv, d, bs, dtype
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_decode_random_batches(gpu, seed):
+    """Seeded random batches: ragged and empty sequences, group sizes for both
+    kernels, head dims 32-128, block sizes 1-64, bf16/fp16."""
+    lens, hq, hkv, d, bs, dtype = _random_decode_case(seed)
+    label = f"random decode seed={seed} B={len(lens)} hq={hq} hkv={hkv} d={d} bs={bs} {dtype}"
+    print(f"case {label} lens={lens}", flush=True)
+    q, kc, vc, table, sl = _make_case(lens, hq, hkv, d, bs, dtype, "cuda", 500 + seed)
+    _check(q, kc, vc, table, sl, label)
