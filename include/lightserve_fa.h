@@ -127,7 +127,10 @@ typedef struct {
   int32_t dtype;
   int32_t batch;
   int32_t heads_q;
-  int32_t heads_kv;            /* must equal heads_q: GQA backward is not implemented */
+  int32_t heads_kv;            /* divides heads_q; below heads_q (GQA: query head h reads KV head
+                                  h / (heads_q / heads_kv), and dk / dv [batch, heads_kv, seqlen_k,
+                                  head_dim] sum over the heads_q / heads_kv query heads of their group)
+                                  only for bf16/fp16 without LSFA_BWD_STORED_DS */
   int32_t seqlen_q;
   int32_t seqlen_k;
   int32_t head_dim;

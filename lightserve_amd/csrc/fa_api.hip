@@ -248,7 +248,10 @@ int lsfa_bwd_check(const lsfa_bwd_args* a) {
   if (rc) return rc;
   if (a->cu_seqlens_q != nullptr || a->cu_seqlens_k != nullptr)
     return fail(LSFA_ERR_UNSUPPORTED, "varlen backward is not implemented");
-  if (a->heads_kv != a->heads_q) return fail(LSFA_ERR_UNSUPPORTED, "GQA backward is not implemented (heads_kv != heads_q)");
+  if (a->heads_kv != a->heads_q && a->dtype == LSFA_DTYPE_FP32)
+    return fail(LSFA_ERR_UNSUPPORTED, "the fp32 backward has no GQA (heads_kv != heads_q)");
+  if (a->heads_kv != a->heads_q && (a->flags & LSFA_BWD_STORED_DS))
+    return fail(LSFA_ERR_UNSUPPORTED, "LSFA_BWD_STORED_DS has no GQA (heads_kv != heads_q)");
   const int phase = a->flags & ~LSFA_BWD_STORED_DS;
   if (phase != 0 && phase != LSFA_BWD_ONLY_DQ && phase != LSFA_BWD_ONLY_DKDV)
     return fail(LSFA_ERR_INVALID, "unknown flags %d", a->flags);
@@ -321,6 +324,7 @@ static int run_bwd(const lsfa_bwd_args* a, void* stream) {
   p.sdvb = a->dv_stride[0]; p.sdvh = a->dv_stride[1]; p.sdvn = a->dv_stride[2]; p.sdvd = a->dv_stride[3];
   p.slb = a->lse_stride[0]; p.slh = a->lse_stride[1]; p.sln = a->lse_stride[2];
   p.B = a->batch; p.H = a->heads_q; p.Nq = a->seqlen_q; p.Nk = a->seqlen_k; p.D = a->head_dim;
+  p.G = a->heads_kv > 0 ? a->heads_q / a->heads_kv : 1;
   p.scale = a->sm_scale;
   p.scale_log2 = a->sm_scale * 1.4426950408889634f;
   const int dp = padded_dim(a->head_dim);

@@ -69,9 +69,10 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   const int q0 = qt * BM;
   const int off = nk - nq;
 
+  const int hk = h / p.G;  // KV head of this query head
   const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
-  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh;
-  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh;
+  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)hk * p.skh;
+  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)hk * p.svh;
   const T* Og = (const T*)p.o + (int64_t)b * p.sob + (int64_t)h * p.soh;
   const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
   T* dQ = (T*)p.dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh;
@@ -293,7 +294,9 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV. Workgroup = 4 waves, one per SIMD, over 128 keys; wave w owns keys
+// dK, dV. Workgroup = 4 waves, one per SIMD, over 128 keys of one KV head
+// (with GQA the tiles of the head's G query heads follow one another through
+// the ring, summing into the same dK/dV registers); wave w owns keys
 // 32w..32w+31 and keeps their K and V rows in registers for the whole kernel
 // (the B operands of S = Q K^T and dP = dO V^T). Q, dO and the rows'
 // L*log2e and -delta blocks stream through three LDS stages of 64-row tiles by
@@ -321,7 +324,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 // contiguous memory. Keys at or past nk are stored as zero, masked (causal)
 // entries are zero already.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, bool CAUSAL, bool DS>
+template <typename T, int DP, bool CAUSAL, bool DS, bool GQA = false>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
@@ -342,24 +345,32 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   const int l32 = lane & 31, hh = lane >> 5;
   const int kb = wave;
   const bool w_hi = wave >= NW / 2;  // waves 2, 3 load dO; 0, 1 load Q
+  // One workgroup per (batch, KV head, key tile). With GQA (G query heads
+  // per KV head) the query tiles of the group's G heads stream through the
+  // ring one head after another, into the same dK/dV sums.
+  static_assert(!(GQA && DS), "the stored-dS path has no GQA");
+  const int G = GQA ? p.G : 1, Hkv = p.H / G;
   int bh, kt;
   map_tile(p.num_tiles, gridDim.x, p.heads_per_group, bh, kt, false);  // low key tiles see the most queries
   bh += p.bh0;
-  const int b = bh / p.H, h = bh - b * p.H;
+  const int b = bh / Hkv, hk = bh - b * Hkv, h0 = hk * G;
   const int nq = p.Nq, nk = p.Nk, D = p.D;
   const int k0 = kt * BNK;
   const int off = nk - nq;
 
-  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)h * p.skh;
-  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)h * p.svh;
-  const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
-  const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
-  const float* LD = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh;
+  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)hk * p.skh;
+  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)hk * p.svh;
+  const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h0 * p.sqh;
+  const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h0 * p.sdoh;
+  const float* LD = p.ld + (int64_t)b * p.sldb + (int64_t)h0 * p.sldh;
 
   const int n_qt = (nq + BMQ - 1) / BMQ;  // every tile starts below nq
   int t_begin = 0;
   if (CAUSAL) t_begin = max(0, k0 - off) / BMQ;  // first tile holding a query that sees key k0
-  const int n_t = max(0, n_qt - t_begin);
+  const int n_t = max(0, n_qt - t_begin);  // visible query tiles per query head
+  const int n_all = G * n_t;               // ... over the group's heads
+  // Linear tile index -> (query head of the group, tile within the head).
+  auto head_of = [&](int tt) { return GQA ? tt / n_t : 0; };
   const int kcol = k0 + 32 * kb + l32;  // this lane's key
 
   // dS blocks: this wave's 32 keys are block row kblk of the head, blocks
@@ -393,18 +404,20 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   int rvo[CR];
 #pragma unroll
   for (int i = 0; i < CR; ++i) rvo[i] = row_voff((wave % (NW / 2)) * CR + i, w_hi ? p.sdon : p.sqn);
-  auto load_tile = [&](int t, int stage, const int* vo) {
-    const int q0 = t * BMQ;
+  auto load_tile = [&](int tt, int stage, const int* vo) {
+    const int g = head_of(tt);
+    const int q0 = (t_begin + tt - g * n_t) * BMQ;
     const int rows = min(nq - q0, BMQ);
     const int64_t sn = w_hi ? p.sdon : p.sqn;
-    const __amdgpu_buffer_rsrc_t rs = tile_rsrc((w_hi ? dO : Q) + (int64_t)q0 * sn, (int)(rows * sn * 2));
+    const T* src = w_hi ? dO + (int64_t)g * p.sdoh : Q + (int64_t)g * p.sqh;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(src + (int64_t)q0 * sn, (int)(rows * sn * 2));
     LDS_AS char* base = sm + stage * RS_B + (w_hi ? R_B : 0);
 #pragma unroll
     for (int i = 0; i < CR; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(base + ((wave % (NW / 2)) * CR + i) * 1024), 16,
                                                vo[i], 0, 0, 0);
     if (wave == 0 && lane < BMQ * 8 / 16) {
-      const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(LD + 2 * (int64_t)q0, BMQ * 8);
+      const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(LD + (int64_t)g * p.sldh + 2 * (int64_t)q0, BMQ * 8);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (LDS_AS void*)(sm + stage * RS_B + 2 * R_B), 16, lane * 16, 0, 0,
                                                0);
     }
@@ -412,7 +425,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   // The first three tiles go in flight before the K / V register loads.
 #pragma unroll
   for (int i = 0; i < NST; ++i)
-    if (i < n_t) load_tile(t_begin + i, i, rvo);
+    if (i < n_all) load_tile(i, i, rvo);
 
   // K and V rows of this lane's key as B operands: columns 16kk + 8hh .. +7.
   X8 kreg[KSTEPS], vreg[KSTEPS];
@@ -642,18 +655,19 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   f32x16 sa, da, sb, db;  // S / dP of the current and the next half
-  if (n_t > 0) scores(sm, 0, sa, da);
+  if (n_all > 0) scores(sm, 0, sa, da);
   // Per tile: the second half's S/dP beside the first half's softmax, the
   // first half's dV/dK; the next tile's first-half S/dP beside the second
   // half's softmax (past the last tile they read a stale stage and are
   // discarded), the second half's dV/dK; then the tile-end barrier: every
   // wave is done with this stage, which takes the tile NST ahead, and the
   // tile loaded at the previous barrier has landed.
-  for (int t0 = 0; t0 < n_t; t0 += NST) {
+  for (int t0 = 0; t0 < n_all; t0 += NST) {
 #pragma unroll
     for (int si = 0; si < NST; ++si) {
-      const int t = t0 + si;
-      if (t >= n_t) break;
+      const int tt = t0 + si;
+      if (tt >= n_all) break;
+      const int t = tt - head_of(tt) * n_t;  // tile within its head (masking, dS blocks)
       const LDS_AS char* stg = sm + si * RS_B;
       const LDS_AS char* nstg = sm + ((si + 1) % NST) * RS_B;
       const bool chi = si == 2, nhi = (si + 1) % NST == 2;
@@ -663,13 +677,13 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
       phase_y(stg, chi, t, 1, sb, db);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (t + NST < n_t) load_tile(t_begin + t + NST, si, rvo);
+      if (tt + NST < n_all) load_tile(tt + NST, si, rvo);
     }
   }
 
   if (kcol < nk) {
-    T* rk = (T*)p.dk + (int64_t)b * p.sdkb + (int64_t)h * p.sdkh + (int64_t)kcol * p.sdkn;
-    T* rv = (T*)p.dv + (int64_t)b * p.sdvb + (int64_t)h * p.sdvh + (int64_t)kcol * p.sdvn;
+    T* rk = (T*)p.dk + (int64_t)b * p.sdkb + (int64_t)hk * p.sdkh + (int64_t)kcol * p.sdkn;
+    T* rv = (T*)p.dv + (int64_t)b * p.sdvb + (int64_t)hk * p.sdvh + (int64_t)kcol * p.sdvn;
     const float sc = p.scale;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -984,9 +998,14 @@ static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   p.num_tiles = (p.Nk + 127) / 128;
-  p.heads_per_group = heads_per_group_for((long long)p.Nq * DP * 2 * 2);  // Q and dO rows of a head
+  // one workgroup per (b, KV head, key tile); it streams the Q and dO rows of the group's G heads
+  p.heads_per_group = heads_per_group_for((long long)p.Nq * DP * 2 * 2 * p.G);
   if ((phases & 2) && p.num_tiles > 0) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
+    const dim3 grid(p.num_tiles * (BH / p.G));
+    if (p.G > 1)
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false, true>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false>), grid, dim3(256), 0, s, p);
     e = hipGetLastError();
   }
   return e;

@@ -199,6 +199,7 @@ struct BwdParams {
   int64_t slb, slh, sln;
   int64_t sqd, skd, svd, sod, sdod, sdqd, sdkd, sdvd;  // fp32 path only
   int B, H, Nq, Nk, D;
+  int G;             // query heads per KV head (GQA: query head h reads KV head h / G)
   int num_tiles;     // tiles per (b, h) along the kernel's stationary axis
   int heads_per_group;  // map_tile grouping
   float scale;       // sm_scale

@@ -185,9 +185,19 @@ def test_abi_backward_validation(built_library):
                         heads_q=4, heads_kv=4, seqlen_q=8, seqlen_k=8, head_dim=64, causal=1,
                         sm_scale=0.125, flags=0)
     assert _lib.bwd_check(args)[0] == 0
+    # GQA (heads_kv dividing heads_q) on the bf16/fp16 default path; not with
+    # the stored-dS path or in fp32; heads_kv must divide heads_q
     args.heads_kv = 2
+    assert _lib.bwd_check(args)[0] == 0
+    args.flags = _lib.BWD_STORED_DS
     rc, msg = _lib.bwd_check(args)
     assert rc == -2 and "GQA" in msg
+    args.flags, args.dtype = 0, _lib.DTYPE_FP32
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -2 and "GQA" in msg and "fp32" in msg
+    args.dtype, args.heads_kv = _lib.DTYPE_BF16, 3
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -1 and "multiple" in msg
     args.heads_kv = 4
     args.workspace = None
     rc, msg = _lib.bwd_check(args)
@@ -232,7 +242,7 @@ def test_abi_backward_noalloc_limit(built_library):
     assert _lib.bwd_workspace_size(args) > _lib.BWD_SCRATCH_BYTES
     rc = _lib.load().lsfa_bwd_noalloc(ctypes.byref(args), None)
     assert rc == -2 and "scratch" in _lib.load().lsfa_last_error().decode()
-    args.heads_kv = 16  # GQA backward: rejected like lsfa_bwd
+    args.heads_kv, args.dtype = 16, _lib.DTYPE_FP32  # the fp32 backward has no GQA: rejected like lsfa_bwd
     args.seqlen_q = args.seqlen_k = 128
     rc = _lib.load().lsfa_bwd_noalloc(ctypes.byref(args), None)
     assert rc == -2 and "GQA" in _lib.load().lsfa_last_error().decode()

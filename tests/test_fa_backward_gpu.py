@@ -118,14 +118,14 @@ def _abi_fwd_bwd(q, k, v, do, causal, scale, phases=(0,), poison=False):
     NaN bytes."""
     from lightserve_amd import _lib
     B, H, Nq, D = q.shape
-    Nk = k.shape[2]
+    Hkv, Nk = k.shape[1], k.shape[2]
     o = torch.empty_like(q)
     L = torch.empty(B, H, Nq, device=q.device, dtype=torch.float32)
     dt = _lib.TORCH_TO_LSFA[q.dtype]
     fa = _lib.FwdArgs(q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), o=o.data_ptr(), lse=L.data_ptr(),
                       q_stride=_lib.strides4(q), k_stride=_lib.strides4(k), v_stride=_lib.strides4(v),
                       o_stride=_lib.strides4(o), lse_stride=_lib._i64x3(*L.stride()),
-                      cu_seqlens_q=None, cu_seqlens_k=None, dtype=dt, batch=B, heads_q=H, heads_kv=H,
+                      cu_seqlens_q=None, cu_seqlens_k=None, dtype=dt, batch=B, heads_q=H, heads_kv=Hkv,
                       seqlen_q=Nq, seqlen_k=Nk, head_dim=D, causal=int(causal), sm_scale=scale, reserved=0)
     stream = _lib.current_stream(q.device)
     _lib.fwd(fa, stream)
@@ -136,7 +136,7 @@ def _abi_fwd_bwd(q, k, v, do, causal, scale, phases=(0,), poison=False):
                       v_stride=_lib.strides4(v), o_stride=_lib.strides4(o), do_stride=_lib.strides4(do),
                       dq_stride=_lib.strides4(dq), dk_stride=_lib.strides4(dk), dv_stride=_lib.strides4(dv),
                       lse_stride=_lib._i64x3(*L.stride()), cu_seqlens_q=None, cu_seqlens_k=None, dtype=dt,
-                      batch=B, heads_q=H, heads_kv=H, seqlen_q=Nq, seqlen_k=Nk, head_dim=D,
+                      batch=B, heads_q=H, heads_kv=Hkv, seqlen_q=Nq, seqlen_k=Nk, head_dim=D,
                       causal=int(causal), sm_scale=scale, flags=phases[0])
     n = _lib.bwd_workspace_size(ba)
     ws = torch.empty(max(n, 1), device=q.device, dtype=torch.uint8)
@@ -277,3 +277,37 @@ def test_long_query_fwd_bwd(gpu, Nq, Nk, causal, dtype):
     8-wave workgroups): ragged ends, rows that see no key, Nq != Nk."""
     print(f"case long-q dq Nq={Nq} Nk={Nk} causal={causal} {dtype}", flush=True)
     _check_fwd_bwd(gpu, 1, 2, Nq, Nk, 128, dtype, causal, Nq + Nk, f"long-q {Nq}x{Nk}")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Nq,Nk,D,causal,dtype", [
+    (2, 8, 2, 300, 300, 128, True, torch.bfloat16), (1, 32, 8, 1024, 1024, 128, True, torch.bfloat16),
+    (2, 6, 3, 200, 333, 64, False, torch.float16), (1, 4, 1, 513, 257, 64, True, torch.bfloat16),
+    (1, 8, 4, 129, 700, 96, True, torch.float16), (3, 4, 2, 77, 77, 32, False, torch.bfloat16),
+    (1, 8, 2, 4160, 4160, 128, True, torch.bfloat16)])
+def test_abi_backward_gqa(gpu, B, Hq, Hkv, Nq, Nk, D, causal, dtype):
+    """GQA backward through the C ABI (query head h reads KV head h / G,
+    G = Hq / Hkv): dQ per query head, dK/dV per KV head summed over its G
+    query heads. Checked against the oracle on K/V repeated G times (as the
+    reference's own GQA convention, repeat_interleave over the head axis),
+    with dK/dV summed over each group."""
+    print(f"case gqa bwd {B}x{Hq}/{Hkv} Nq={Nq} Nk={Nk} D={D} causal={causal} {dtype}", flush=True)
+    G = Hq // Hkv
+    g = torch.Generator().manual_seed(Nq + 7 * Hq)
+    q, do = (torch.randn(B, Hq, Nq, D, generator=g).to(dtype) for _ in range(2))
+    k, v = (torch.randn(B, Hkv, Nk, D, generator=g).to(dtype) for _ in range(2))
+    scale = D ** -0.5
+    o, L, dq, dk, dv = _abi_fwd_bwd(*(t.to(gpu) for t in (q, k, v, do)), causal, scale, poison=True)
+    torch.cuda.synchronize()
+    ke, ve = k.repeat_interleave(G, dim=1), v.repeat_interleave(G, dim=1)
+    o_ref, l_ref = attention_reference(q, ke, ve, causal, scale)
+    what = f"gqa {Hq}/{Hkv} {Nq}x{Nk}"
+    assert_lse(L.cpu(), l_ref, f"{what} L")
+    seen = torch.isfinite(l_ref)
+    assert_gate(o.cpu().double()[seen], o_ref[seen], f"{what} o")
+    grp = lambda t: t.reshape(B, Hkv, G, Nk, D).sum(2)  # noqa: E731
+    dq_e, dk_e, dv_e = attention_grads(q, ke, ve, do, causal, scale)
+    dq_a, dk_a, dv_a = flash_backward_tiled(q, ke, ve, o_ref.nan_to_num().to(dtype), l_ref, do, causal, scale,
+                                            op_dtype=dtype)
+    for name, got, ex, ra in (("dq", dq, dq_e, dq_a), ("dk", dk, grp(dk_e), grp(dk_a)), ("dv", dv, grp(dv_e), grp(dv_a))):
+        assert got.shape == ex.shape, name
+        assert_grad_parity(got.cpu(), ex.nan_to_num(), ra.nan_to_num(), f"{what} {name}")
