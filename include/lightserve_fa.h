@@ -122,7 +122,11 @@ typedef struct {
   int64_t dk_stride[4];
   int64_t dv_stride[4];
   int64_t lse_stride[3];
-  const int32_t* cu_seqlens_q; /* must be NULL: varlen backward is not implemented */
+  const int32_t* cu_seqlens_q; /* NULL, or packed varlen as in lsfa_fwd_args (bf16/fp16 without
+                                  LSFA_BWD_STORED_DS): q/o/dout/dq rows of sequence b at
+                                  cu_seqlens_q[b] .., k/v/dk/dv rows at cu_seqlens_k[b] .., strides
+                                  [0, head, row, 1], lse [heads_q, total_q], seqlen_q / seqlen_k the
+                                  longest sequences (longer ones are clamped to them) */
   const int32_t* cu_seqlens_k;
   int32_t dtype;
   int32_t batch;

@@ -246,8 +246,13 @@ int lsfa_bwd_check(const lsfa_bwd_args* a) {
   if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
   int rc = check_common(a->dtype, a->batch, a->heads_q, a->heads_kv, a->seqlen_q, a->seqlen_k, a->head_dim, a->sm_scale);
   if (rc) return rc;
-  if (a->cu_seqlens_q != nullptr || a->cu_seqlens_k != nullptr)
-    return fail(LSFA_ERR_UNSUPPORTED, "varlen backward is not implemented");
+  if ((a->cu_seqlens_q == nullptr) != (a->cu_seqlens_k == nullptr))
+    return fail(LSFA_ERR_INVALID, "cu_seqlens_q and cu_seqlens_k must both be set or both be NULL");
+  const bool varlen = a->cu_seqlens_q != nullptr;
+  if (varlen && a->dtype == LSFA_DTYPE_FP32)
+    return fail(LSFA_ERR_UNSUPPORTED, "the fp32 backward has no varlen (cu_seqlens)");
+  if (varlen && (a->flags & LSFA_BWD_STORED_DS))
+    return fail(LSFA_ERR_UNSUPPORTED, "LSFA_BWD_STORED_DS has no varlen (cu_seqlens)");
   if (a->heads_kv != a->heads_q && a->dtype == LSFA_DTYPE_FP32)
     return fail(LSFA_ERR_UNSUPPORTED, "the fp32 backward has no GQA (heads_kv != heads_q)");
   if (a->heads_kv != a->heads_q && (a->flags & LSFA_BWD_STORED_DS))
@@ -281,7 +286,7 @@ int lsfa_bwd_check(const lsfa_bwd_args* a) {
       const int64_t* strides[8] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride,
                                    a->do_stride, a->dq_stride, a->dk_stride, a->dv_stride};
       for (int i = 0; i < 8; ++i)
-        if ((rc = check_fast_layout(names[i], ptrs[i], strides[i], false))) return rc;
+        if ((rc = check_fast_layout(names[i], ptrs[i], strides[i], varlen))) return rc;
     }
   }
   return ok();
@@ -325,6 +330,8 @@ static int run_bwd(const lsfa_bwd_args* a, void* stream) {
   p.slb = a->lse_stride[0]; p.slh = a->lse_stride[1]; p.sln = a->lse_stride[2];
   p.B = a->batch; p.H = a->heads_q; p.Nq = a->seqlen_q; p.Nk = a->seqlen_k; p.D = a->head_dim;
   p.G = a->heads_kv > 0 ? a->heads_q / a->heads_kv : 1;
+  p.cu_q = a->cu_seqlens_q;
+  p.cu_k = a->cu_seqlens_k;
   p.scale = a->sm_scale;
   p.scale_log2 = a->sm_scale * 1.4426950408889634f;
   const int dp = padded_dim(a->head_dim);

@@ -44,7 +44,7 @@ constexpr int kCacheNT = 2;
 //   dS^T = P^T (dP^T - delta)  -> rounded into B operands
 //   dQ^T += K^T dS^T      A = K^T via transpose reads of the same LDS tile
 // ---------------------------------------------------------------------------
-template <typename T, int DP, bool CAUSAL>
+template <typename T, int DP, bool CAUSAL, bool VARLEN = false>
 __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
@@ -65,17 +65,29 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   int bh, qt;
   map_tile(p.num_tiles, gridDim.x, p.heads_per_group, bh, qt, CAUSAL);
   const int b = bh / p.H, h = bh - b * p.H;
-  const int nq = p.Nq, nk = p.Nk, D = p.D;
+  int nq = p.Nq, nk = p.Nk;
+  int64_t rq0 = 0, rk0 = 0;  // varlen: the sequence's first query / key row
+  if (VARLEN) {  // lengths clamped to the longest the grid and the workspace were sized for
+    rq0 = p.cu_q[b];
+    nq = min(max(p.cu_q[b + 1] - (int)rq0, 0), p.Nq);
+    rk0 = p.cu_k[b];
+    nk = min(max(p.cu_k[b + 1] - (int)rk0, 0), p.Nk);
+  }
+  const int D = p.D;
   const int q0 = qt * BM;
+  // Past this sequence's queries (varlen grids cover the longest one); its
+  // workspace rows are never read. Uniform, before any barrier.
+  if (VARLEN && q0 >= nq) return;
   const int off = nk - nq;
 
   const int hk = h / p.G;  // KV head of this query head
-  const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
-  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)hk * p.skh;
-  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)hk * p.svh;
-  const T* Og = (const T*)p.o + (int64_t)b * p.sob + (int64_t)h * p.soh;
-  const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h * p.sdoh;
-  T* dQ = (T*)p.dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh;
+  const int64_t bq = VARLEN ? 0 : b, bk = VARLEN ? 0 : b;
+  const T* Q = (const T*)p.q + bq * p.sqb + (int64_t)h * p.sqh + rq0 * p.sqn;
+  const T* K = (const T*)p.k + bk * p.skb + (int64_t)hk * p.skh + rk0 * p.skn;
+  const T* V = (const T*)p.v + bk * p.svb + (int64_t)hk * p.svh + rk0 * p.svn;
+  const T* Og = (const T*)p.o + bq * p.sob + (int64_t)h * p.soh + rq0 * p.son;
+  const T* dO = (const T*)p.dout + bq * p.sdob + (int64_t)h * p.sdoh + rq0 * p.sdon;
+  T* dQ = (T*)p.dq + bq * p.sdqb + (int64_t)h * p.sdqh + rq0 * p.sdqn;
 
   const int qw_lo = q0 + wave * 32;
   const int qrow = qw_lo + l32;
@@ -129,7 +141,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
     if (qvalid && col < D) oraw[kk] = ldg16(Og + (int64_t)qrow * p.son + col);
   }
   float lraw = -INFINITY;
-  if (qvalid) lraw = p.lse[(int64_t)b * p.slb + (int64_t)h * p.slh + (int64_t)qrow * p.sln];
+  if (qvalid) lraw = p.lse[bq * p.slb + (int64_t)h * p.slh + (rq0 + qrow) * p.sln];
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
@@ -324,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 // contiguous memory. Keys at or past nk are stored as zero, masked (causal)
 // entries are zero already.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, bool CAUSAL, bool DS, bool GQA = false>
+template <typename T, int DP, bool CAUSAL, bool DS, bool GQA = false, bool VARLEN = false>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
   using X4 = typename VecT<T>::x4;
@@ -348,20 +360,30 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   // One workgroup per (batch, KV head, key tile). With GQA (G query heads
   // per KV head) the query tiles of the group's G heads stream through the
   // ring one head after another, into the same dK/dV sums.
-  static_assert(!(GQA && DS), "the stored-dS path has no GQA");
+  static_assert(!((GQA || VARLEN) && DS), "the stored-dS path has no GQA or varlen");
   const int G = GQA ? p.G : 1, Hkv = p.H / G;
   int bh, kt;
   map_tile(p.num_tiles, gridDim.x, p.heads_per_group, bh, kt, false);  // low key tiles see the most queries
   bh += p.bh0;
   const int b = bh / Hkv, hk = bh - b * Hkv, h0 = hk * G;
-  const int nq = p.Nq, nk = p.Nk, D = p.D;
+  int nq = p.Nq, nk = p.Nk;
+  int64_t rq0 = 0, rk0 = 0;  // varlen: the sequence's first query / key row
+  if (VARLEN) {  // lengths clamped to the longest the grid and the workspace were sized for
+    rq0 = p.cu_q[b];
+    nq = min(max(p.cu_q[b + 1] - (int)rq0, 0), p.Nq);
+    rk0 = p.cu_k[b];
+    nk = min(max(p.cu_k[b + 1] - (int)rk0, 0), p.Nk);
+  }
+  const int D = p.D;
   const int k0 = kt * BNK;
+  if (VARLEN && k0 >= nk) return;  // past this sequence's keys; uniform, before any barrier
   const int off = nk - nq;
 
-  const T* K = (const T*)p.k + (int64_t)b * p.skb + (int64_t)hk * p.skh;
-  const T* V = (const T*)p.v + (int64_t)b * p.svb + (int64_t)hk * p.svh;
-  const T* Q = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h0 * p.sqh;
-  const T* dO = (const T*)p.dout + (int64_t)b * p.sdob + (int64_t)h0 * p.sdoh;
+  const int64_t bb = VARLEN ? 0 : b;
+  const T* K = (const T*)p.k + bb * p.skb + (int64_t)hk * p.skh + rk0 * p.skn;
+  const T* V = (const T*)p.v + bb * p.svb + (int64_t)hk * p.svh + rk0 * p.svn;
+  const T* Q = (const T*)p.q + bb * p.sqb + (int64_t)h0 * p.sqh + rq0 * p.sqn;
+  const T* dO = (const T*)p.dout + bb * p.sdob + (int64_t)h0 * p.sdoh + rq0 * p.sdon;
   const float* LD = p.ld + (int64_t)b * p.sldb + (int64_t)h0 * p.sldh;
 
   const int n_qt = (nq + BMQ - 1) / BMQ;  // every tile starts below nq
@@ -682,8 +704,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   }
 
   if (kcol < nk) {
-    T* rk = (T*)p.dk + (int64_t)b * p.sdkb + (int64_t)hk * p.sdkh + (int64_t)kcol * p.sdkn;
-    T* rv = (T*)p.dv + (int64_t)b * p.sdvb + (int64_t)hk * p.sdvh + (int64_t)kcol * p.sdvn;
+    T* rk = (T*)p.dk + bb * p.sdkb + (int64_t)hk * p.sdkh + (rk0 + kcol) * p.sdkn;
+    T* rv = (T*)p.dv + bb * p.sdvb + (int64_t)hk * p.sdvh + (rk0 + kcol) * p.sdvn;
     const float sc = p.scale;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -993,8 +1015,12 @@ static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
   p.nbh = BH;
   p.num_tiles = (p.Nq + 127) / 128;
   p.heads_per_group = heads_per_group_for((long long)p.Nk * DP * 2 * 2);  // K and V rows of a head
+  const bool varlen = p.cu_q != nullptr;  // grids over the longest sequence; shorter ones exit early
   if ((phases & 1) && p.num_tiles > 0) {
-    hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
+    if (varlen)
+      hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL, true>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP, CAUSAL>), dim3(p.num_tiles * BH), dim3(256), 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   p.num_tiles = (p.Nk + 127) / 128;
@@ -1002,7 +1028,11 @@ static hipError_t launch_bwd(BwdParams p, int phases, hipStream_t s) {
   p.heads_per_group = heads_per_group_for((long long)p.Nq * DP * 2 * 2 * p.G);
   if ((phases & 2) && p.num_tiles > 0) {
     const dim3 grid(p.num_tiles * (BH / p.G));
-    if (p.G > 1)
+    if (varlen && p.G > 1)
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false, true, true>), grid, dim3(256), 0, s, p);
+    else if (varlen)
+      hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false, false, true>), grid, dim3(256), 0, s, p);
+    else if (p.G > 1)
       hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false, true>), grid, dim3(256), 0, s, p);
     else
       hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP, CAUSAL, false>), grid, dim3(256), 0, s, p);

@@ -200,6 +200,10 @@ struct BwdParams {
   int64_t sqd, skd, svd, sod, sdod, sdqd, sdkd, sdvd;  // fp32 path only
   int B, H, Nq, Nk, D;
   int G;             // query heads per KV head (GQA: query head h reads KV head h / G)
+  // Varlen (packed [tokens, heads, d] rows; Nq / Nk are the longest
+  // sequences): sequence b's rows are cu_q[b] .. cu_q[b+1]-1 (cu_k for keys)
+  const int32_t* cu_q;
+  const int32_t* cu_k;
   int num_tiles;     // tiles per (b, h) along the kernel's stationary axis
   int heads_per_group;  // map_tile grouping
   float scale;       // sm_scale

@@ -63,3 +63,61 @@ def flash_attention_varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seql
     if ok is not o:
         o.copy_(ok[..., :D])
     return o, lse
+
+
+def flash_attention_varlen_backward(do, q, k, v, o, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                    causal=True, sm_scale=None):
+    """Gradients of the packed varlen (and GQA) forward: returns (dq, dk, dv)
+    in the inputs' dtype and layout, dk/dv per KV head summed over its group.
+    lse is the forward's [Hq, total_q] fp32 output. bf16/fp16 with head dims
+    that are multiples of 8 (the fp32 kernels have no varlen backward)."""
+    assert q.dtype in (torch.bfloat16, torch.float16), "the varlen backward runs on bf16/fp16"
+    assert q.shape[2] % 8 == 0, "the varlen backward needs a head dim that is a multiple of 8"
+    assert do.shape == q.shape == o.shape and k.shape == v.shape and do.dtype == q.dtype
+    assert lse.dtype == torch.float32 and lse.shape == (q.shape[1], q.shape[0])
+    Tq, Hq, D = q.shape
+    Tk, Hkv = k.shape[0], k.shape[1]
+    batch = cu_seqlens_q.numel() - 1
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
+    q, k, v, o, do = (t.contiguous() for t in (q, k, v, o, do))
+    lse = lse.contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    if Tq == 0 and Tk == 0:
+        return dq, dk, dv
+    cu_q = cu_seqlens_q.contiguous()
+    cu_k = cu_seqlens_k.contiguous()
+    th = _lib.strides_thd
+    args = _lib.BwdArgs(
+        q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), o=o.data_ptr(), dout=do.data_ptr(), lse=lse.data_ptr(),
+        dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(), workspace=None, workspace_bytes=0,
+        q_stride=th(q), k_stride=th(k), v_stride=th(v), o_stride=th(o), do_stride=th(do), dq_stride=th(dq),
+        dk_stride=th(dk), dv_stride=th(dv), lse_stride=_lib._i64x3(0, lse.stride(0), lse.stride(1)),
+        cu_seqlens_q=cu_q.data_ptr(), cu_seqlens_k=cu_k.data_ptr(), dtype=_lib.TORCH_TO_LSFA[q.dtype],
+        batch=batch, heads_q=Hq, heads_kv=Hkv, seqlen_q=int(max_seqlen_q), seqlen_k=int(max_seqlen_k),
+        head_dim=D, causal=int(bool(causal)), sm_scale=scale, flags=0)
+    n = _lib.bwd_workspace_size(args)
+    ws = torch.empty(max(n, 1), device=q.device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), n
+    with torch.cuda.device(q.device):
+        _lib.bwd(args, _lib.current_stream(q.device))
+    return dq, dk, dv
+
+
+class _VarlenFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, causal, sm_scale):
+        o, lse = flash_attention_varlen_forward(q, k, v, cu_q, cu_k, max_q, max_k, causal, sm_scale)
+        ctx.save_for_backward(q, k, v, o, lse, cu_q, cu_k)
+        ctx.cfg = (max_q, max_k, causal, sm_scale)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse, cu_q, cu_k = ctx.saved_tensors
+        dq, dk, dv = flash_attention_varlen_backward(do, q, k, v, o, lse, cu_q, cu_k, *ctx.cfg)
+        return dq, dk, dv, None, None, None, None, None, None
+
+
+def flash_attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, causal=True, sm_scale=None):
+    """Differentiable packed varlen / GQA attention: o [total_q, Hq, D]."""
+    return _VarlenFunction.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, causal, sm_scale)

@@ -203,10 +203,19 @@ def test_abi_backward_validation(built_library):
     rc, msg = _lib.bwd_check(args)
     assert rc == -1
     args.workspace = 4096
+    # varlen (cu_seqlens) on the bf16/fp16 default path only; both or neither
     args.cu_seqlens_q = 16
     args.cu_seqlens_k = 32
+    assert _lib.bwd_check(args)[0] == 0
+    args.flags = _lib.BWD_STORED_DS
     rc, msg = _lib.bwd_check(args)
     assert rc == -2 and "varlen" in msg
+    args.flags, args.dtype = 0, _lib.DTYPE_FP32
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -2 and "varlen" in msg
+    args.dtype, args.cu_seqlens_k = _lib.DTYPE_BF16, None
+    rc, msg = _lib.bwd_check(args)
+    assert rc == -1 and "cu_seqlens" in msg
     args.cu_seqlens_q = args.cu_seqlens_k = None
     # flags: at most one phase (LSFA_BWD_ONLY_DQ / ONLY_DKDV), with or without
     # LSFA_BWD_STORED_DS; the fp32 path takes no phase (STORED_DS is ignored)

@@ -172,3 +172,62 @@ def test_varlen_random_batches(gpu):
         o_ref, lse_ref = varlen_reference(q, k, v, cu_q, cu_k, causal=causal)
         assert_gate(o.cpu(), o_ref, f"varlen random {case}")
         assert_lse(lse.cpu(), lse_ref, f"varlen random {case}")
+
+
+def _varlen_grad_reference(q, k, v, do, lens_q, lens_k, causal, scale):
+    """Per sequence: the oracle's forward and float64 gradients on K/V
+    repeated over each group (query head h reads KV head h // G), dK/dV
+    summed over the group; plus the reference algorithm's gradients."""
+    from oracle.attention import attention_grads, attention_reference, flash_backward_tiled
+    Hq, Hkv, D = q.shape[1], k.shape[1], q.shape[2]
+    G = Hq // Hkv
+    outs = {n: [] for n in ("o", "dq", "dk", "dv", "aq", "ak", "av")}
+    cq = ck = 0
+    for nq, nk in zip(lens_q, lens_k):
+        qb, dob = (t[cq:cq + nq].transpose(0, 1)[None] for t in (q, do))
+        kb, vb = (t[ck:ck + nk].transpose(0, 1)[None].repeat_interleave(G, dim=1) for t in (k, v))
+        o_r, l_r = attention_reference(qb, kb, vb, causal, scale)
+        ex = attention_grads(qb, kb, vb, dob, causal, scale)
+        al = flash_backward_tiled(qb, kb, vb, o_r.nan_to_num().to(q.dtype), l_r, dob, causal, scale, op_dtype=q.dtype)
+        grp = lambda t: t.reshape(1, Hkv, G, nk, D).sum(2)[0].transpose(0, 1)  # noqa: E731
+        outs["o"].append(o_r.nan_to_num()[0].transpose(0, 1))
+        outs["dq"].append(ex[0].nan_to_num()[0].transpose(0, 1))
+        outs["aq"].append(al[0].nan_to_num()[0].transpose(0, 1))
+        outs["dk"].append(grp(ex[1].nan_to_num()))
+        outs["ak"].append(grp(al[1].nan_to_num()))
+        outs["dv"].append(grp(ex[2].nan_to_num()))
+        outs["av"].append(grp(al[2].nan_to_num()))
+        cq += nq
+        ck += nk
+    return {n: torch.cat(v, dim=0) for n, v in outs.items()}
+
+
+@pytest.mark.parametrize("lens_q,lens_k,Hq,Hkv,D,causal,dtype", [
+    ([300, 0, 77, 513], [300, 40, 200, 513], 8, 2, 128, True, torch.bfloat16),
+    ([128, 1000, 64], [1100, 1000, 0], 4, 4, 64, True, torch.float16),
+    ([17, 250, 129], [400, 250, 33], 6, 3, 96, False, torch.bfloat16),
+    ([1, 700, 2], [1, 900, 5], 32, 8, 128, True, torch.float16),
+    ([4160, 96], [4160, 300], 4, 1, 128, True, torch.bfloat16)])
+def test_varlen_backward(gpu, lens_q, lens_k, Hq, Hkv, D, causal, dtype):
+    """Packed varlen (and GQA) forward + backward through the autograd
+    wrapper against the oracle per sequence (bottom-right causal, empty
+    sequences, Nq != Nk, rows that see no key)."""
+    from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen
+    from tests.gates import assert_grad_parity
+    print(f"case varlen bwd lens_q={lens_q} lens_k={lens_k} {Hq}/{Hkv} D={D} causal={causal} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(sum(lens_q) + Hq)
+    Tq, Tk = sum(lens_q), sum(lens_k)
+    q, do = (torch.randn(Tq, Hq, D, generator=g).to(dtype) for _ in range(2))
+    k, v = (torch.randn(Tk, Hkv, D, generator=g).to(dtype) for _ in range(2))
+    cu = lambda ls: torch.tensor([0] + list(torch.tensor(ls).cumsum(0)), dtype=torch.int32, device=gpu)  # noqa: E731
+    scale = D ** -0.5
+    qg, kg, vg = (t.to(gpu).requires_grad_() for t in (q, k, v))
+    o = flash_attention_varlen(qg, kg, vg, cu(lens_q), cu(lens_k), max(lens_q), max(lens_k), causal, scale)
+    o.backward(do.to(gpu))
+    torch.cuda.synchronize()
+    ref = _varlen_grad_reference(q, k, v, do, lens_q, lens_k, causal, scale)
+    assert_gate(o.detach().cpu(), ref["o"], "varlen o")
+    for name, got, ex, al in (("dq", qg.grad, ref["dq"], ref["aq"]), ("dk", kg.grad, ref["dk"], ref["ak"]),
+                              ("dv", vg.grad, ref["dv"], ref["av"])):
+        assert got.shape == ex.shape, name
+        assert_grad_parity(got.cpu(), ex, al, f"varlen {name}")
