@@ -82,8 +82,8 @@ def flash_attention_varlen_backward(do, q, k, v, o, lse, cu_seqlens_q, cu_seqlen
     q, k, v, o, do = (t.contiguous() for t in (q, k, v, o, do))
     lse = lse.contiguous()
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    if Tq == 0 and Tk == 0:
-        return dq, dk, dv
+    if Tq == 0 or Tk == 0:  # no query sees a key: every gradient is zero
+        return dq.zero_(), dk.zero_(), dv.zero_()
     cu_q = cu_seqlens_q.contiguous()
     cu_k = cu_seqlens_k.contiguous()
     th = _lib.strides_thd
