@@ -231,3 +231,15 @@ def test_varlen_backward(gpu, lens_q, lens_k, Hq, Hkv, D, causal, dtype):
                               ("dv", vg.grad, ref["dv"], ref["av"])):
         assert got.shape == ex.shape, name
         assert_grad_parity(got.cpu(), ex, al, f"varlen {name}")
+
+
+def test_varlen_backward_no_queries(gpu):
+    """A batch with no query rows: every gradient is zero (no launch)."""
+    from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen_backward
+    q = torch.empty(0, 4, 64, device=gpu, dtype=torch.bfloat16)
+    k, v = (torch.randn(50, 2, 64, device=gpu).bfloat16() for _ in range(2))
+    lse = torch.empty(4, 0, device=gpu, dtype=torch.float32)
+    cu_q = torch.zeros(3, dtype=torch.int32, device=gpu)
+    cu_k = torch.tensor([0, 20, 50], dtype=torch.int32, device=gpu)
+    dq, dk, dv = flash_attention_varlen_backward(q, q, k, v, q, lse, cu_q, cu_k, 0, 30, True)
+    assert dq.shape == q.shape and torch.count_nonzero(dk) == 0 and torch.count_nonzero(dv) == 0
