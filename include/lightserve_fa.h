@@ -468,7 +468,8 @@ int lsfa_fwd(const lsfa_fwd_args* args, void* stream);
 int lsfa_bwd_check(const lsfa_bwd_args* args);
 
 /* Workspace bytes lsfa_bwd needs for these arguments (only dtype, flags,
- * batch, heads_q, seqlen_q and seqlen_k matter); no GPU work. */
+ * batch, heads_q, seqlen_q, seqlen_k and head_dim matter: head_dim decides
+ * whether LSFA_BWD_STORED_DS applies); no GPU work. */
 int lsfa_bwd_workspace_size(const lsfa_bwd_args* args, uint64_t* bytes);
 
 /* Backward: delta, then dk, dv and dq. Replaces the preprocess launch

@@ -4,7 +4,8 @@
 
 Every source is compiled for gfx950 only, in parallel, with packed-fp32 VALU
 instructions disabled, then linked into lightserve_amd/liblsfa_gfx950.so next
-to the Python package that loads it.
+to the Python package that loads it; the linker's version script
+(exports.map) exports the lsfa_* C ABI and nothing else.
 """
 import concurrent.futures
 import os
@@ -68,7 +69,9 @@ def build(verbose=False):
             print(err, file=sys.stderr)
     objs = [o for o, _ in results]
     tmp = OUT + ".tmp"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    # exports.map keeps the dynamic symbol table to the lsfa_* C ABI
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC",
+           f"-Wl,--version-script={os.path.join(HERE, 'exports.map')}", *objs, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"linking failed:\n{' '.join(cmd)}\n{proc.stderr}")

@@ -362,6 +362,8 @@ int lsfa_bwd(const lsfa_bwd_args* a, void* stream) {
 // call (with the device current) and kept in scratch_ptr.
 static __device__ __attribute__((aligned(256))) char scratch[LSFA_BWD_SCRATCH_BYTES];
 
+}  // extern "C"
+
 namespace {
 constexpr int kMaxDevices = 64;
 std::mutex scratch_mutex;
@@ -384,6 +386,8 @@ int scratch_for_current_device(void** out) {
   return LSFA_OK;
 }
 }  // namespace
+
+extern "C" {
 
 int lsfa_bwd_noalloc(const lsfa_bwd_args* args, void* stream) {
   if (args == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");
@@ -571,6 +575,10 @@ int lsfa_prefill_paged(const lsfa_prefill_paged_args* a, void* stream) {
   return ok();
 }
 
+}  // extern "C"
+
+namespace {
+
 // Skinny GEMM split: about 1024 workgroups (256 columns x one K-range each)
 // with K-ranges of at least 128 rows (multiples of 8; measured on MI355X in
 // graph replays: 1024 workgroups with 128-row minimum beat 256-4096
@@ -646,6 +654,10 @@ long long gemv_total_n(const lsfa_gemv_group_args* a) {
   for (int i = 0; i < std::min(std::max(a->count, 0), LSFA_GEMV_MAX_GROUP); ++i) n += std::max(a->n[i], 0);
   return n;
 }
+
+}  // namespace
+
+extern "C" {
 
 int lsfa_gemv_group_check(const lsfa_gemv_group_args* a) {
   if (a == nullptr) return fail(LSFA_ERR_INVALID, "args is NULL");

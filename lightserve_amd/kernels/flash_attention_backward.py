@@ -84,8 +84,12 @@ def _flash_attention_backward(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor
 
 
 class _FlashAttentionFunction(torch.autograd.Function):
+    """The reference's autograd Function (kernels/flash_attention_backward.py:385-397):
+    `_FlashAttentionFunction.apply(q, k, v, causal)` as there, with sm_scale
+    an optional fifth argument (default 1/sqrt(D))."""
+
     @staticmethod
-    def forward(ctx, q, k, v, causal, sm_scale):
+    def forward(ctx, q, k, v, causal, sm_scale=None):
         o, L = _flash_attention_forward_lse(q, k, v, causal, sm_scale)
         ctx.save_for_backward(q, k, v, o, L)
         ctx.causal = causal

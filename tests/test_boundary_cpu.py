@@ -72,6 +72,27 @@ def test_varlen_validation():
         flash_attention_varlen_forward(q[None], k, k, cu, cu, 8, 10)
 
 
+def test_varlen_backward_validation_cpu():
+    """The varlen backward and the differentiable varlen entry point validate
+    before touching the library: host tensors, 4-D inputs and groupless head
+    counts raise AssertionError in a GPU-less process."""
+    from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen, flash_attention_varlen_backward
+    q = torch.randn(8, 4, 16, dtype=torch.bfloat16)
+    k = torch.randn(10, 2, 16, dtype=torch.bfloat16)
+    lse = torch.zeros(4, 8)
+    cu = torch.tensor([0, 8], dtype=torch.int32)
+    cu_k = torch.tensor([0, 10], dtype=torch.int32)
+    with pytest.raises(AssertionError):  # host tensors
+        flash_attention_varlen_backward(q, q, k, k, q, lse, cu, cu_k, 8, 10)
+    with pytest.raises(AssertionError):  # 4-D input
+        flash_attention_varlen_backward(q[None], q[None], k, k, q[None], lse, cu, cu_k, 8, 10)
+    k3 = torch.randn(10, 3, 16, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):  # 4 query heads over 3 kv heads
+        flash_attention_varlen_backward(q, q, k3, k3, q, lse, cu, cu_k, 8, 10)
+    with pytest.raises(AssertionError):
+        flash_attention_varlen(q.requires_grad_(), k, k, cu, cu_k, 8, 10)
+
+
 def test_import_loads_no_native_code():
     """Importing the package must not need the library or a GPU (the
     reference's CI runs validation tests on CPU-only runners)."""
@@ -94,6 +115,22 @@ def test_library_exports_every_declared_symbol(built_library):
     for name in declared:
         assert hasattr(lib, name), name
     assert _lib.load().lsfa_abi_version() == _lib.ABI_VERSION
+
+
+def test_library_exports_nothing_else(built_library):
+    """The dynamic symbol table holds exactly the declared C ABI: no host
+    helper, kernel stub or C++ symbol leaks out of the drop-in library (the
+    compiler's __hip_cuid_* markers aside)."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("no nm")
+    out = subprocess.run([nm, "-D", "--defined-only", built_library], capture_output=True, text=True,
+                         check=True).stdout
+    names = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    names = {n for n in names if not n.startswith("__hip_cuid_")}
+    assert names == set(_lib.EXPORTED_SYMBOLS), sorted(names ^ set(_lib.EXPORTED_SYMBOLS))
 
 
 def test_struct_layout_matches_header(built_library):
@@ -639,3 +676,41 @@ def test_rmsnorm_and_matmul_validation_cpu():
         matmul(torch.randn(2, 3), torch.randn(4, 5))
     with pytest.raises(AssertionError):  # CPU tensors
         matmul(torch.randn(2, 3), torch.randn(3, 5))
+
+
+def _integration_stub():
+    """The reference-side ctypes stub of INTEGRATION.md section 2, as text."""
+    import os
+    import re
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "INTEGRATION.md")
+    blocks = re.findall(r"```python\n(.*?)```", open(path).read(), flags=re.S)
+    stub = [b for b in blocks if b.startswith("# kernels/_lsfa.py")]
+    assert len(stub) == 1, "INTEGRATION.md must hold one ctypes stub starting '# kernels/_lsfa.py'"
+    return stub[0]
+
+
+def test_integration_stub_binds_this_library(built_library):
+    """The documented stub runs against the built library: its ABI assertion
+    holds, its FwdArgs has the header's layout (field by field against the
+    package's mirror), and an argument block it builds passes lsfa_fwd_check
+    (host-only validation, no GPU), while a bad head dim is refused."""
+    code = _integration_stub().replace("/path/to/lightserve_amd/liblsfa_gfx950.so", built_library)
+    ns = {}
+    exec(compile(code, "INTEGRATION.md stub", "exec"), ns)  # runs its `assert lsfa_abi_version() == ...`
+    Stub = ns["FwdArgs"]
+    assert ctypes.sizeof(Stub) == ctypes.sizeof(_lib.FwdArgs)
+    for (name, _), (mname, _) in zip(Stub._fields_, _lib.FwdArgs._fields_):
+        assert name == mname and getattr(Stub, name).offset == getattr(_lib.FwdArgs, mname).offset, name
+    lib = ns["_lib"]
+    lib.lsfa_fwd_check.argtypes = [ctypes.POINTER(Stub)]
+    lib.lsfa_fwd_check.restype = ctypes.c_int
+    B, H, N, D = 2, 4, 64, 128
+    st = (H * N * D, N * D, D, 1)
+    ptr = 1 << 20  # aligned placeholder: the check never dereferences it
+    a = Stub(q=ptr, k=ptr, v=ptr, o=ptr, lse=None, q_stride=ns["_i64x4"](*st), k_stride=ns["_i64x4"](*st),
+             v_stride=ns["_i64x4"](*st), o_stride=ns["_i64x4"](*st), lse_stride=ns["_i64x3"](0, 0, 0),
+             cu_seqlens_q=None, cu_seqlens_k=None, dtype=ns["_DT"][torch.bfloat16], batch=B, heads_q=H,
+             heads_kv=H, seqlen_q=N, seqlen_k=N, head_dim=D, causal=1, sm_scale=D ** -0.5, reserved=0)
+    assert lib.lsfa_fwd_check(ctypes.byref(a)) == 0, lib.lsfa_last_error()
+    a.head_dim = 12
+    assert lib.lsfa_fwd_check(ctypes.byref(a)) != 0

@@ -11,7 +11,8 @@ import pytest
 import torch
 
 from lightserve_amd.kernels.flash_attention import flash_attention_forward
-from lightserve_amd.kernels.flash_attention_backward import (_flash_attention_backward, _flash_attention_forward_lse,
+from lightserve_amd.kernels.flash_attention_backward import (_backward_args, _flash_attention_backward,
+                                                             _flash_attention_forward_lse, _FlashAttentionFunction,
                                                              flash_attention)
 from oracle.attention import attention_grads, attention_reference, flash_backward_tiled
 from lightserve_amd.workloads import make_config_inputs
@@ -28,6 +29,20 @@ def test_gradcheck(gpu, B, H, N, D, causal):
     torch.manual_seed(0)
     q, k, v = (torch.randn(B, H, N, D, device=gpu, dtype=torch.float32, requires_grad=True) for _ in range(3))
     assert torch.autograd.gradcheck(lambda a, b, c: flash_attention(a, b, c, causal=causal), (q, k, v),
+                                    eps=1e-3, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_apply_signature(gpu, causal):
+    """The reference calls `_FlashAttentionFunction.apply(q, k, v, causal)`
+    (kernels/flash_attention_backward.py:385-397, :420): four arguments, no
+    scale. Gradcheck through that exact call, and the same output as the
+    entry point."""
+    torch.manual_seed(3)
+    q, k, v = (torch.randn(1, 2, 9, 16, device=gpu, dtype=torch.float32, requires_grad=True) for _ in range(3))
+    out = _FlashAttentionFunction.apply(q, k, v, causal)
+    torch.testing.assert_close(out, flash_attention(q, k, v, causal=causal), atol=0, rtol=0)
+    assert torch.autograd.gradcheck(lambda a, b, c: _FlashAttentionFunction.apply(a, b, c, causal), (q, k, v),
                                     eps=1e-3, atol=1e-2, rtol=1e-2)
 
 
@@ -86,17 +101,32 @@ def _grads_gpu_fp32(q, k, v, do, causal):
     return attention_grads(q, k, v, do, causal, dtype=torch.float32)
 
 
-@pytest.mark.parametrize("cfg", [3, 4])
-def test_config_backward_full_size(gpu, cfg):
+def _backward_with_flags(do, q, k, v, o, L, causal, flags):
+    """_flash_attention_backward with lsfa_bwd_args.flags set (equal head dims
+    that need no padding: the outputs are written in place)."""
+    from lightserve_amd import _lib
+    args, keep = _backward_args(do, q, k, v, o, L, causal, flags=flags)
+    assert all(a is b for a, b in zip(keep[:3], keep[3])), "needs an unpadded, kernel-ready layout"
+    _lib.bwd(args, _lib.current_stream(q.device))
+    return keep[:3]
+
+
+@pytest.mark.parametrize("cfg,stored", [(3, False), (4, False), (3, True)])
+def test_config_backward_full_size(gpu, cfg, stored):
     """The max-abs / mean-abs gate on dQ/dK/dV at the full config size, on every
     (batch, head) slice, with the oracle's fp32 autograd on the GPU (a gradient
     that misses the gate must be within 1.5x of the reference algorithm's own
-    error, tests/gates.py)."""
-    print(f"case config {cfg} backward full size", flush=True)
+    error, tests/gates.py). stored: the opt-in stored-dS path
+    (LSFA_BWD_STORED_DS), checked against the oracle the same way."""
+    from lightserve_amd import _lib
+    print(f"case config {cfg} backward full size stored_ds={stored}", flush=True)
     inp = make_config_inputs(cfg, device=gpu)
     q, k, v, do, causal = inp["q"], inp["k"], inp["v"], inp["do"], inp["causal"]
     o, L = _flash_attention_forward_lse(q, k, v, causal)
-    dq, dk, dv = _flash_attention_backward(do, q, k, v, o, L, causal)
+    if stored:
+        dq, dk, dv = _backward_with_flags(do, q, k, v, o, L, causal, _lib.BWD_STORED_DS)
+    else:
+        dq, dk, dv = _flash_attention_backward(do, q, k, v, o, L, causal)
     slices = [(b, h) for b in range(q.shape[0]) for h in range(q.shape[1])]
     for b, h in slices:
         sl = (slice(b, b + 1), slice(h, h + 1))
@@ -238,16 +268,17 @@ def _random_case(seed):
     return B, H, Nq, Nk, D, dtype, r.random() < 0.5
 
 
-def _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, seed, what):
+def _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, seed, what, flags=0):
     """Forward with L and backward through the C ABI (workspace poisoned with
-    NaN bytes) against the oracle: L and o under the forward gate (rows that
-    see no key: L = -inf, o = 0), dQ/dK/dV against the float64 autograd under
-    the gradient gate."""
+    NaN bytes; lsfa_bwd_args.flags = flags) against the oracle: L and o under
+    the forward gate (rows that see no key: L = -inf, o = 0), dQ/dK/dV against
+    the float64 autograd under the gradient gate."""
     g = torch.Generator().manual_seed(1000 + seed)
     q, do = (torch.randn(B, H, Nq, D, generator=g).to(dtype) for _ in range(2))
     k, v = (torch.randn(B, H, Nk, D, generator=g).to(dtype) for _ in range(2))
     scale = D ** -0.5
-    o, L, dq, dk, dv = _abi_fwd_bwd(*(t.to(gpu) for t in (q, k, v, do)), causal, scale, poison=True)
+    o, L, dq, dk, dv = _abi_fwd_bwd(*(t.to(gpu) for t in (q, k, v, do)), causal, scale, phases=(flags,),
+                                    poison=True)
     torch.cuda.synchronize()
     o_ref, l_ref = attention_reference(q, k, v, causal, scale)
     assert_lse(L.cpu(), l_ref, f"{what} L")
@@ -259,6 +290,21 @@ def _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, seed, what):
                                    op_dtype=dtype)
     for name, got, ex, ra in zip(("dq", "dk", "dv"), (dq, dk, dv), exact, ref_alg):
         assert_grad_parity(got.cpu(), ex.nan_to_num(), ra.nan_to_num(), f"{what} {name}")
+
+
+@pytest.mark.parametrize("B,H,Nq,Nk,causal,dtype", [
+    (2, 3, 300, 300, True, torch.bfloat16), (1, 2, 700, 333, True, torch.bfloat16),
+    (1, 2, 333, 700, True, torch.float16), (2, 2, 513, 513, False, torch.bfloat16),
+    (1, 3, 1, 129, True, torch.bfloat16), (1, 2, 1100, 77, False, torch.float16)])
+def test_stored_ds_oracle(gpu, B, H, Nq, Nk, causal, dtype):
+    """The stored-dS path (LSFA_BWD_STORED_DS, head dim 128: dS written by the
+    dK/dV kernel, dQ a GEMM over it) against the float64 oracle under the
+    gradient gate, on the non-square causal shapes whose unwritten dS blocks
+    the dQ GEMM must mask, with the workspace poisoned."""
+    from lightserve_amd import _lib
+    print(f"case stored-dS oracle {B}x{H} Nq={Nq} Nk={Nk} causal={causal} {dtype}", flush=True)
+    _check_fwd_bwd(gpu, B, H, Nq, Nk, 128, dtype, causal, Nq * 7 + Nk, f"stored-dS {Nq}x{Nk}",
+                   flags=_lib.BWD_STORED_DS)
 
 
 @pytest.mark.parametrize("seed", range(24))

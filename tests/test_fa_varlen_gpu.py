@@ -207,11 +207,14 @@ def _varlen_grad_reference(q, k, v, do, lens_q, lens_k, causal, scale):
     ([128, 1000, 64], [1100, 1000, 0], 4, 4, 64, True, torch.float16),
     ([17, 250, 129], [400, 250, 33], 6, 3, 96, False, torch.bfloat16),
     ([1, 700, 2], [1, 900, 5], 32, 8, 128, True, torch.float16),
-    ([4160, 96], [4160, 300], 4, 1, 128, True, torch.bfloat16)])
+    ([4160, 96], [4160, 300], 4, 1, 128, True, torch.bfloat16),
+    ([90, 33], [120, 33], 4, 2, 12, True, torch.bfloat16),
+    ([65, 200], [65, 150], 2, 1, 40, False, torch.float16)])
 def test_varlen_backward(gpu, lens_q, lens_k, Hq, Hkv, D, causal, dtype):
     """Packed varlen (and GQA) forward + backward through the autograd
     wrapper against the oracle per sequence (bottom-right causal, empty
-    sequences, Nq != Nk, rows that see no key)."""
+    sequences, Nq != Nk, rows that see no key, head dims the wrapper pads to a
+    multiple of 8 in both directions)."""
     from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen
     from tests.gates import assert_grad_parity
     print(f"case varlen bwd lens_q={lens_q} lens_k={lens_k} {Hq}/{Hkv} D={D} causal={causal} {dtype}", flush=True)
@@ -243,3 +246,37 @@ def test_varlen_backward_no_queries(gpu):
     cu_k = torch.tensor([0, 20, 50], dtype=torch.int32, device=gpu)
     dq, dk, dv = flash_attention_varlen_backward(q, q, k, v, q, lse, cu_q, cu_k, 0, 30, True)
     assert dq.shape == q.shape and torch.count_nonzero(dk) == 0 and torch.count_nonzero(dv) == 0
+
+
+def test_varlen_backward_validation(gpu):
+    """The varlen backward makes the forward's checks before any launch:
+    int64 or host cu_seqlens, unequal cu_seqlens lengths, head counts that
+    do not group, a wrong lse shape; fp32 inputs that require grad are refused
+    by the differentiable entry point before its forward runs."""
+    from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen, flash_attention_varlen_backward
+    q = torch.randn(40, 4, 64, device=gpu).bfloat16()
+    k = torch.randn(50, 2, 64, device=gpu).bfloat16()
+    lse = torch.zeros(4, 40, device=gpu)
+    cu_q = torch.tensor([0, 20, 40], dtype=torch.int32, device=gpu)
+    cu_k = torch.tensor([0, 20, 50], dtype=torch.int32, device=gpu)
+    bad = [
+        dict(cu_seqlens_q=cu_q.long()),
+        dict(cu_seqlens_k=cu_k.cpu()),
+        dict(cu_seqlens_k=cu_k[:2]),
+        dict(k=torch.randn(50, 3, 64, device=gpu).bfloat16(), v=torch.randn(50, 3, 64, device=gpu).bfloat16()),
+        dict(lse=torch.zeros(40, 4, device=gpu)),
+        dict(do=q.cpu()),
+    ]
+    for over in bad:
+        a = dict(do=q, q=q, k=k, v=k, o=q, lse=lse, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=20,
+                 max_seqlen_k=30)
+        a.update(over)
+        with pytest.raises(AssertionError):
+            flash_attention_varlen_backward(**a)
+    qf = torch.randn(40, 4, 64, device=gpu, requires_grad=True)
+    kf = torch.randn(50, 2, 64, device=gpu)
+    with pytest.raises(AssertionError):
+        flash_attention_varlen(qf, kf, kf, cu_q, cu_k, 20, 30)
+    with torch.no_grad():  # no gradient wanted: the fp32 forward runs
+        o = flash_attention_varlen(qf, kf, kf, cu_q, cu_k, 20, 30)
+    assert o.shape == qf.shape
