@@ -85,6 +85,8 @@ def parse_args():
                          "rmsnorm: fused residual add + RMSNorm, [2048, 8192] bf16; "
                          "sweep: B=1 H=32 D=128 bf16 over N 512-8192 beside torch's SDPA")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="config 3: skip the compact runs of configs 2, 4 and 5 added to its line")
     ap.add_argument("--skip-parity", action="store_true",
                     help="skip the oracle re-check before timing (profiler runs only, whose per-kernel counters "
                          "should cover the timed kernels; the JSON line then says parity was not checked)")
@@ -111,8 +113,9 @@ def measured_traffic(kernel, workload):
     return None
 
 
-def check_parity(cfg, inp, outs):
-    """Oracle check of every (batch, head) slice (fp32 oracle on the GPU).
+def check_parity(cfg, inp, outs, slices=None):
+    """Oracle check of every (batch, head) slice (fp32 oracle on the GPU), or
+    of the given (batch, head) slices.
 
     o and lse against the closed form; dq/dk/dv against fp32 autograd. The
     gate is max-abs <= 2e-2 and mean-abs <= 2e-3 (lse max-abs <= 1e-3); a
@@ -132,19 +135,20 @@ def check_parity(cfg, inp, outs):
         st[1] += err.mean().item()
         st[2] += 1
 
-    for b in range(B):
-        for h in range(H):
-            sl = (slice(b, b + 1), slice(h, h + 1))
-            o_ref, lse_ref = attention_reference(q[sl], k[sl], v[sl], causal, dtype=torch.float32)
-            add("o", outs["o"][sl], o_ref)
-            add("lse", outs["lse"][sl], lse_ref)
-            if "dq" in outs:
-                exact = attention_grads(q[sl], k[sl], v[sl], inp["do"][sl], causal, dtype=torch.float32)
-                alg = flash_backward_tiled(q[sl], k[sl], v[sl], o_ref.to(q.dtype), lse_ref, inp["do"][sl], causal,
-                                           block_n=256, op_dtype=q.dtype)
-                for name, ex, ra in zip(("dq", "dk", "dv"), exact, alg):
-                    add(name, outs[name][sl], ex)
-                    add(name + "_ref_alg", ra.to(q.dtype), ex)
+    if slices is None:
+        slices = [(b, h) for b in range(B) for h in range(H)]
+    for b, h in slices:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        o_ref, lse_ref = attention_reference(q[sl], k[sl], v[sl], causal, dtype=torch.float32)
+        add("o", outs["o"][sl], o_ref)
+        add("lse", outs["lse"][sl], lse_ref)
+        if "dq" in outs:
+            exact = attention_grads(q[sl], k[sl], v[sl], inp["do"][sl], causal, dtype=torch.float32)
+            alg = flash_backward_tiled(q[sl], k[sl], v[sl], o_ref.to(q.dtype), lse_ref, inp["do"][sl], causal,
+                                       block_n=256, op_dtype=q.dtype)
+            for name, ex, ra in zip(("dq", "dk", "dv"), exact, alg):
+                add(name, outs[name][sl], ex)
+                add(name + "_ref_alg", ra.to(q.dtype), ex)
     res = {n: {"max_abs": float(f"{m:.3e}"), "mean_abs": float(f"{t / c:.3e}")} for n, (m, t, c) in stats.items()}
     ok = res["o"]["max_abs"] <= 2e-2 and res["o"]["mean_abs"] <= 2e-3 and res["lse"]["max_abs"] <= 1e-3
     for name in ("dq", "dk", "dv"):
@@ -156,7 +160,7 @@ def check_parity(cfg, inp, outs):
         r["rule"] = "gate" if gate else ("1.5x reference algorithm" if rel else "failed")
         r["reference_algorithm"] = a
         ok = ok and (gate or rel)
-    res["slices_checked"] = B * H
+    res["slices_checked"] = len(slices)
     return ok, res
 
 
@@ -207,6 +211,115 @@ def cpu_baseline(cfg, inp, n_heads, flops_full, step_kind):
                    f"(1 warm-up, median of 5: {t:.2f} s), scaled linearly; os.cpu_count()={os.cpu_count()}; "
                    f"{cpu_model}"),
     }
+
+
+# (batch, head) slices the compact runs of configs 2 and 4 check against the oracle
+OTHER_CONFIG_SLICES = {2: [(0, 0), (1, 9), (2, 18), (3, 31)], 4: [(0, 0), (0, 5), (0, 10), (0, 15)]}
+
+
+def other_configs(steps, warmup):
+    """Configs 2, 4 and 5 timed back to back after the headline config, each
+    the way --config N times it (W warm-up steps continued until 200 ms of GPU
+    work, then `steps` steps between one event pair; config 4's forward share
+    from a second pass with an event between forward and backward), with
+    parity on a fixed sample: four (batch, head) slices of configs 2 and 4
+    (o, lse; dq/dk/dv at config 4) and two whole sequences of config 5 (o and
+    lse of every query head). Compact: no CPU baseline, no per-kernel split."""
+    import torch
+    from lightserve_amd.kernels.flash_attention_backward import (_flash_attention_backward,
+                                                                 _flash_attention_forward_lse)
+    from lightserve_amd.kernels.flash_attention_varlen import flash_attention_varlen_forward
+    from lightserve_amd.workloads import CONFIGS, bwd_flops, fwd_flops, make_config_inputs, make_varlen_inputs, \
+        varlen_fwd_flops
+    from oracle.attention import attention_reference
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    for c in (2, 4, 5):
+        cfg = CONFIGS[c]
+        t_cfg = time.perf_counter()
+        if c == 5:
+            inp = make_varlen_inputs(device=dev)
+            q, k, v = inp["q"], inp["k"], inp["v"]
+            cu_q, cu_k = inp["cu_seqlens_q"], inp["cu_seqlens_k"]
+            f_fwd = varlen_fwd_flops(cu_q.cpu(), cu_k.cpu(), cfg["Hq"], cfg["D"])
+            f_step, bwd = f_fwd, None
+
+            def fwd():
+                return flash_attention_varlen_forward(q, k, v, cu_q, cu_k, inp["max_seqlen_q"], inp["max_seqlen_k"])
+        else:
+            inp = make_config_inputs(c, device=dev)
+            q, k, v, causal = inp["q"], inp["k"], inp["v"], inp["causal"]
+            f_fwd = fwd_flops(*q.shape, causal)
+            f_step = f_fwd + (bwd_flops(*q.shape, causal) if cfg["backward"] else 0)
+
+            def fwd():
+                return _flash_attention_forward_lse(q, k, v, causal)
+            bwd = (lambda o, lse: _flash_attention_backward(inp["do"], q, k, v, o, lse, causal)) \
+                if cfg["backward"] else None
+        o, lse = fwd()
+        outs = {"o": o, "lse": lse}
+        if bwd is not None:
+            outs["dq"], outs["dk"], outs["dv"] = bwd(o, lse)
+        torch.cuda.synchronize()
+        if c == 5:
+            cq, ck = cu_q.tolist(), cu_k.tolist()
+            G = cfg["Hq"] // cfg["Hkv"]
+            worst = {"o": [0.0, 0.0], "lse": [0.0, 0.0]}
+            for b in (0, len(cq) - 2):
+                qb = q[cq[b]:cq[b + 1]].transpose(0, 1)[None]
+                kb = k[ck[b]:ck[b + 1]].transpose(0, 1).repeat_interleave(G, 0)[None]
+                vb = v[ck[b]:ck[b + 1]].transpose(0, 1).repeat_interleave(G, 0)[None]
+                o_ref, l_ref = attention_reference(qb, kb, vb, True, dtype=torch.float32)
+                for name, got, ref in (("o", o[cq[b]:cq[b + 1]].transpose(0, 1)[None], o_ref),
+                                       ("lse", lse[:, cq[b]:cq[b + 1]][None], l_ref)):
+                    err = (got.double() - ref.double()).abs()
+                    worst[name] = [max(worst[name][0], err.max().item()), max(worst[name][1], err.mean().item())]
+            parity = {n: {"max_abs": float(f"{w[0]:.3e}"), "mean_abs": float(f"{w[1]:.3e}")} for n, w in worst.items()}
+            parity["sequences_checked"] = 2
+            ok = worst["o"][0] <= 2e-2 and worst["o"][1] <= 2e-3 and worst["lse"][0] <= 1e-3
+        else:
+            ok, parity = check_parity(cfg, inp, outs, OTHER_CONFIG_SLICES[c])
+        del outs
+
+        def step():
+            o, lse = fwd()
+            if bwd is not None:
+                bwd(o, lse)
+
+        warm_up(step, warmup, stream)
+        h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        h0.record(stream)
+        for _ in range(steps):
+            step()
+        h1.record(stream)
+        torch.cuda.synchronize()
+        ms = h0.elapsed_time(h1) / steps
+        tf = f_step / (ms * 1e-3) / 1e12
+        r = {"workload": cfg["name"], "step": "fwd+bwd" if bwd is not None else "fwd",
+             "ms_per_step": round(ms, 5), "tflops": round(tf, 2), "pct_of_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2)}
+        if bwd is not None:
+            ev = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
+            torch.cuda.synchronize()
+            for e0, e1, e2 in ev:
+                e0.record(stream)
+                o, lse = fwd()
+                e1.record(stream)
+                bwd(o, lse)
+                e2.record(stream)
+            torch.cuda.synchronize()
+            fms = sum(a.elapsed_time(b) for a, b, _ in ev) / steps
+            bms = sum(b.elapsed_time(c) for _, b, c in ev) / steps
+            r["fwd"] = {"ms": round(fms, 5), "pct_of_peak": round(100 * f_fwd / (fms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)}
+            fb = f_step - f_fwd
+            r["bwd"] = {"ms": round(bms, 5), "pct_of_peak": round(100 * fb / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)}
+        r["parity"] = {"ok": bool(ok), **parity}
+        r["wall_s"] = round(time.perf_counter() - t_cfg, 2)
+        out[f"config{c}"] = r
+        del inp, q, k, v, o, lse
+        torch.cuda.empty_cache()
+    return out
 
 
 def calibration_copy(dev, mib):
@@ -765,8 +878,11 @@ def bench_sweep(args):
     scaled_dot_product_attention forced onto its flash backend (the
     memory-efficient backend if flash cannot run; the line names which).
     Forward: the inference entry point (flash_attention_forward, no
-    logsumexp) against SDPA; forward+backward: the training pair
-    (forward with L, lsfa_bwd) against SDPA under autograd. Outputs and
+    logsumexp) against SDPA; backward alone: .backward(retain_graph=True)
+    on a graph built once (the reference's backward benchmark,
+    kernels/benchmark_flash_attention_backward.py:89-107), flash_attention
+    against SDPA; forward+backward: the training pair (forward with L,
+    lsfa_bwd) against SDPA under autograd. Outputs and
     gradients are compared with the vendor's before each shape is timed.
     Timing: 10 warm-up calls, then the median of 5 blocks of 30 calls
     (HIP events)."""
@@ -774,7 +890,8 @@ def bench_sweep(args):
     import torch
     import torch.nn.functional as F
     from lightserve_amd.kernels.flash_attention import flash_attention_forward
-    from lightserve_amd.kernels.flash_attention_backward import _flash_attention_backward, _flash_attention_forward_lse
+    from lightserve_amd.kernels.flash_attention_backward import (_flash_attention_backward,
+                                                                 _flash_attention_forward_lse, flash_attention)
     from lightserve_amd.workloads import bwd_flops, fwd_flops
     dev = torch.device("cuda", 0)
     try:
@@ -850,6 +967,29 @@ def bench_sweep(args):
                 gerr = max((a.float() - b.grad.float()).abs().max().item() for a, b in ((dq, qg), (dk, kg), (dv, vg)))
                 row["grad_max_abs_vs_vendor"] = round(gerr, 5)
                 row["grad_ok"] = gerr <= 5e-2
+            # backward alone, as the reference's backward benchmark times it
+            # (kernels/benchmark_flash_attention_backward.py:89-107): the graph
+            # is built once by one forward, then only .backward(retain_graph=True)
+            # is timed
+            f_bwd = bwd_flops(B, H, n, D, causal)
+
+            def backward_step(fn):
+                qb, kb, vb = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+                out = fn(qb, kb, vb)
+
+                def run():
+                    qb.grad = kb.grad = vb.grad = None
+                    out.backward(do, retain_graph=True)
+                return run
+            ms = timed(backward_step(lambda a, b, c: flash_attention(a, b, c, causal=causal)))
+            row["bwd_ms"] = round(ms, 5)
+            row["bwd_tflops"] = round(f_bwd / (ms * 1e-3) / 1e12, 2)
+            if ref is not None:
+                vms = timed(backward_step(lambda a, b, c: vendor(a, b, c, causal, vbe)))
+                row["vendor_bwd_ms"] = round(vms, 5)
+                row["vendor_bwd_tflops"] = round(f_bwd / (vms * 1e-3) / 1e12, 2)
+                row["bwd_pct_of_vendor"] = round(100 * vms / ms, 1)
+            row["bwd_pct_of_peak"] = round(100 * row["bwd_tflops"] / PEAK_BF16_TFLOPS, 2)
             ms = timed(ours_step)
             row["fwd_bwd_ms"] = round(ms, 5)
             row["fwd_bwd_tflops"] = round(f_step / (ms * 1e-3) / 1e12, 2)
@@ -861,7 +1001,8 @@ def bench_sweep(args):
             row["fwd_bwd_pct_of_peak"] = round(100 * row["fwd_bwd_tflops"] / PEAK_BF16_TFLOPS, 2)
             rows.append(row)
             print(f"sweep {row['shape']} causal={causal}: fwd {row['fwd_tflops']} TF/s "
-                  f"({row.get('fwd_pct_of_vendor', '-')}% of vendor), fwd+bwd {row['fwd_bwd_tflops']} TF/s "
+                  f"({row.get('fwd_pct_of_vendor', '-')}% of vendor), bwd {row['bwd_tflops']} TF/s "
+                  f"({row.get('bwd_pct_of_vendor', '-')}% of vendor), fwd+bwd {row['fwd_bwd_tflops']} TF/s "
                   f"({row.get('fwd_bwd_pct_of_vendor', '-')}% of vendor)", file=sys.stderr, flush=True)
             del q, k, v, do, ours, ref
     gm = math.exp(sum(math.log(r["fwd_tflops"]) for r in rows) / len(rows))
@@ -1129,6 +1270,10 @@ def main():
                              "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2)}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, inp, args.cpu_heads, f_step, step_kind) if args.config != 5 else None
+    if args.config == 3 and not args.no_other_configs:
+        del inp, q, k, v
+        torch.cuda.empty_cache()
+        result["other_configs"] = other_configs(args.steps, args.warmup)
     print(json.dumps(result), flush=True)
 
 
