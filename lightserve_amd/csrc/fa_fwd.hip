@@ -453,13 +453,18 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   }
   __syncthreads();  // K buffer 0 is refilled by the first step
   // One pipelined step: tile t's scores are in cur, tile t+1's go to nxt.
+  // The V load of dense launches is issued after the S MFMAs: each wave's
+  // direct loads queue behind the whole workgroup's in the CU's load path
+  // (issuing all of a step's loads at its start stalled every wave for
+  // ~400 cycles), and V tile t+1 is first needed one step later.
   auto pipe_step = [&](int t, f32x16* cur, f32x16* nxt) {
     if (t + 2 < ntiles) tile_load(K, p.skn, p.skb, p.skh, kvo, t + 2, t & 1, blk2);
-    if (t + 1 < ntiles) tile_load(V, p.svn, p.svb, p.svh, vvo, t + 1, 2 + ((t + 1) & 1), blk1);
+    if (PAGED && t + 1 < ntiles) tile_load(V, p.svn, p.svb, p.svh, vvo, t + 1, 2 + ((t + 1) & 1), blk1);
     if (t + 1 < ntiles && wave_sees(t + 1)) {
       scores(kbuf(t + 1), nxt);
       mask_tile(t + 1, nxt);
     }
+    if (!PAGED && t + 1 < ntiles) tile_load(V, p.svn, p.svb, p.svh, vvo, t + 1, 2 + ((t + 1) & 1), blk1);
     if (wave_sees(t)) {
       X8 pb[2 * KB];
       softmax_checked(cur, pb);
