@@ -140,6 +140,14 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   // Paged: a wave's rows must lie in one cache block (blocks hold 16 or more
   // tokens, a power of two).
   static_assert(!PAGED || (RPW * DP * 2 == LDI * 1024 && (RPW == 8 || RPW == 16)), "rows per wave");
+  // Dense 8-wave launches: the second wave of each SIMD (waves 4-7) issues
+  // the whole tile, 2 LDI chunks each, and waves 0-3 issue none (0.7-2%
+  // faster at the config-3/4 shapes than every wave issuing LDI: a wave
+  // stalls while the CU's load path takes its chunks, and waves 0-3, which
+  // win the SIMD's issue arbitration, then run on). Paged launches keep one
+  // cache block per wave's rows, so every wave loads there.
+  constexpr bool kSecondLoads = NW == 8 && !PAGED;
+  constexpr int LDC = kSecondLoads ? 2 * LDI : LDI;  // 1 KB chunks this wave issues per tile
 
   __shared__ __attribute__((aligned(1024))) T smem_raw[4 * TILE];  // K0 K1 V0 V1
   LDS_AS T* smem = (LDS_AS T*)smem_raw;
@@ -148,6 +156,8 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31, hh = lane >> 5;
+  const bool loads = !kSecondLoads || wave >= NW / 2;  // wave-uniform
+  const int lw = kSecondLoads ? (wave & (NW / 2 - 1)) : wave;  // this wave's chunk group
   int b, h, qt;
   if (VARLEN && p.B <= 64) {
     // Varlen sequences differ in length: workgroup L takes the item of rank
@@ -214,16 +224,16 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
     qreg[kk] = __builtin_bit_cast(X8, raw);
   }
 
-  // Direct global -> LDS tile load: wave w issues LDI 1 KB chunks (tile rows
-  // RPW w .. RPW w + RPW-1); lane t of chunk c lands at tile byte (w*LDI + c)*1024 + 16t
+  // Direct global -> LDS tile load: a loading wave with chunk group g issues
+  // LDC 1 KB chunks; lane t of chunk c lands at tile byte (g*LDC + c)*1024 + 16t
   // = (row, swizzled seg). The buffer descriptor is rebuilt per tile (scalar
   // work) and clipped to the rows that exist, so the per-lane byte offsets
   // are loop-invariant and rows at or past nk (and columns at or past D) read
   // as zero. Paged offsets are relative to the wave's first row.
-  int kvo[LDI], vvo[LDI];
+  int kvo[LDC], vvo[LDC];
 #pragma unroll
-  for (int c = 0; c < LDI; ++c) {
-    const int byte = (wave * LDI + c) * 1024 + lane * 16;
+  for (int c = 0; c < LDC; ++c) {
+    const int byte = (lw * LDC + c) * 1024 + lane * 16;
     const int row = byte / (DP * 2);
     const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
     const int r = PAGED ? row - RPW * wave : row;
@@ -244,6 +254,7 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   };
   auto tile_load = [&](const T* base, int64_t sn, int64_t sblk, int64_t shead, const int* vo, int j, int buf,
                        int blk) {
+    if (!loads) return;
     __amdgpu_buffer_rsrc_t rs;
     if (PAGED) {
       const int key0 = j * BN + RPW * wave;  // wave-uniform
@@ -259,8 +270,8 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
     }
     LDS_AS char* dst = (LDS_AS char*)(smem + buf * TILE);
 #pragma unroll
-    for (int c = 0; c < LDI; ++c)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(dst + (wave * LDI + c) * 1024), 16, vo[c], 0, 0, 0);
+    for (int c = 0; c < LDC; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(dst + (lw * LDC + c) * 1024), 16, vo[c], 0, 0, 0);
   };
 
   // Per-lane LDS byte offsets relative to a tile base. The swizzle depends
@@ -338,7 +349,9 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   auto softmax = [&](const f32x16* s, X8* pb) -> float2 {
     constexpr bool kF16 = std::is_same<T, _Float16>::value;
     const float neg_m = -m_run;
-    float rs[4] = {0.f, 0.f, 0.f, 0.f}, re[4] = {0.f, 0.f, 0.f, 0.f};
+    // The partial sums start at -0, the additive identity, so that the
+    // first add of each folds away (+0 would not: +0 + -0 is +0).
+    float rs[4] = {-0.f, -0.f, -0.f, -0.f}, re[4] = {-0.f, -0.f, -0.f, -0.f};
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       f32x16 p;
