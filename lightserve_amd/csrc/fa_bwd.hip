@@ -208,7 +208,10 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  for (int j = 0; j < ntiles; ++j) {
+  // One key tile j; the loop below runs it twice per iteration (j even,
+  // then odd), so the buffer parity is known at compile time and every LDS
+  // operand address is a lane offset plus an immediate.
+  auto key_tile = [&](int j) {
     if (j + 1 < ntiles) {
       tile_load(K, p.skn, kvo, j + 1, (j + 1) & 1);
       tile_load(V, p.svn, vvo, j + 1, 2 + ((j + 1) & 1));
@@ -284,7 +287,13 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+  };
+  int j = 0;
+  for (; j + 1 < ntiles; j += 2) {
+    key_tile(j);
+    key_tile(j + 1);
   }
+  if (j < ntiles) key_tile(j);
 
   if (qvalid) {
     T* row = dQ + (int64_t)qrow * p.sdqn;
