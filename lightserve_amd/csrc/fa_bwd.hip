@@ -295,21 +295,29 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   }
   if (j < ntiles) key_tile(j);
 
-  if (qvalid) {
-    T* row = dQ + (int64_t)qrow * p.sdqn;
+  // dQ (times sm_scale) leaves through LDS, four whole rows per store
+  // instruction (as dK/dV below); the loop's closing barrier has retired
+  // every K/V read.
+  {
+    constexpr int BLK = 32 * DP * 2;  // bytes of one wave's 32 rows
+    LDS_AS char* wb = sm + wave * BLK;
     const float sc = p.scale;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d = 32 * dt + 8 * g + 4 * hh;
-        if (d < D) {
-          X4 v;
+        X4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (T)(acc[dt][4 * g + e] * sc);
-          *(X4*)(row + d) = v;
-        }
+        for (int e = 0; e < 4; ++e) v[e] = (T)(acc[dt][4 * g + e] * sc);
+        *(LDS_AS X4*)(wb + swz_off<DP>(l32, 32 * dt + 8 * g + 4 * hh) * 2) = v;
       }
+#pragma unroll
+    for (int c = 0; c < BLK / 1024; ++c) {
+      const int byte = c * 1024 + lane * 16;
+      const int row = byte / (DP * 2), seg = (byte % (DP * 2)) / 16;
+      const X8 v = *(const LDS_AS X8*)(wb + row * DP * 2 + ((seg ^ seg_swz<DP>(row)) << 4));
+      const int q = qw_lo + row;
+      if (q < nq && seg * 8 < D) *(X8*)(dQ + (int64_t)q * p.sdqn + seg * 8) = v;
     }
   }
 }
@@ -712,26 +720,45 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     }
   }
 
-  if (kcol < nk) {
-    T* rk = (T*)p.dk + bb * p.sdkb + (int64_t)hk * p.sdkh + (rk0 + kcol) * p.sdkn;
-    T* rv = (T*)p.dv + bb * p.sdvb + (int64_t)hk * p.sdvh + (rk0 + kcol) * p.sdvn;
+  // dK (times sm_scale) and dV leave through LDS: a lane's accumulators hold
+  // 4-column pieces of one key's row, so direct stores would scatter 8-byte
+  // pieces over 32 rows per instruction. Each wave writes its two 32-row
+  // blocks (swizzled 16-byte segments) into its own LDS region, reads them
+  // back row-major and stores 16 bytes per lane, four whole rows per
+  // instruction. The loop's closing barrier has retired every ring read.
+  {
+    constexpr int BLK = 32 * DP * 2;  // bytes of one 32-row block
+    LDS_AS char* wb = sm + wave * 2 * BLK;
     const float sc = p.scale;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d = 32 * dt + 8 * g + 4 * hh;
-        if (d < D) {
-          X4 ck, cv;
+        X4 ck, cv;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            ck[e] = (T)(dk[dt][4 * g + e] * sc);
-            cv[e] = (T)dv[dt][4 * g + e];
-          }
-          *(X4*)(rk + d) = ck;
-          *(X4*)(rv + d) = cv;
+        for (int e = 0; e < 4; ++e) {
+          ck[e] = (T)(dk[dt][4 * g + e] * sc);
+          cv[e] = (T)dv[dt][4 * g + e];
         }
+        const int o = swz_off<DP>(l32, 32 * dt + 8 * g + 4 * hh) * 2;
+        *(LDS_AS X4*)(wb + o) = ck;
+        *(LDS_AS X4*)(wb + BLK + o) = cv;
       }
+    T* rk = (T*)p.dk + bb * p.sdkb + (int64_t)hk * p.sdkh + rk0 * p.sdkn;
+    T* rv = (T*)p.dv + bb * p.sdvb + (int64_t)hk * p.sdvh + rk0 * p.sdvn;
+#pragma unroll
+    for (int c = 0; c < BLK / 1024; ++c) {
+      const int byte = c * 1024 + lane * 16;
+      const int row = byte / (DP * 2), seg = (byte % (DP * 2)) / 16;
+      const int o = row * DP * 2 + ((seg ^ seg_swz<DP>(row)) << 4);
+      const X8 vk = *(const LDS_AS X8*)(wb + o);
+      const X8 vv = *(const LDS_AS X8*)(wb + BLK + o);
+      const int key = k0 + 32 * kb + row;
+      if (key < nk && seg * 8 < D) {
+        *(X8*)(rk + (int64_t)key * p.sdkn + seg * 8) = vk;
+        *(X8*)(rv + (int64_t)key * p.sdvn + seg * 8) = vv;
+      }
+    }
   }
 }
 

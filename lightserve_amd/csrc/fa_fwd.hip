@@ -152,6 +152,7 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   __shared__ __attribute__((aligned(1024))) T smem_raw[4 * TILE];  // K0 K1 V0 V1
   LDS_AS T* smem = (LDS_AS T*)smem_raw;
   const LDS_AS char* sbytes = (const LDS_AS char*)smem_raw;
+  LDS_AS char* smem_bytes = (LDS_AS char*)smem_raw;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -502,21 +503,35 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
 
   const float lt = half_sum(l_run);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (qrow < nq) {
-    T* orow = O + (int64_t)qrow * p.son;
+  // O leaves through LDS: a lane's accumulators hold 4-column pieces of one
+  // query's row, so direct stores would scatter 8-byte pieces over 32 rows
+  // per instruction. Each wave writes its 32 rows (swizzled 16-byte
+  // segments) into its own LDS region, reads them back row-major and stores
+  // 16 bytes per lane, four whole rows per instruction. The last step's
+  // closing barrier has retired every K/V read.
+  {
+    constexpr int BLK = 32 * DP * 2;  // bytes of one wave's 32 rows
+    static_assert(NW * BLK <= 4 * TILE * 2, "O staging fits in the K/V buffers");
+    LDS_AS char* wb = smem_bytes + wave * BLK;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d = 32 * dt + 8 * g + 4 * hh;
-        if (d < D) {
-          X4 v;
+        X4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (T)(acc[dt][4 * g + e] * inv);
-          *(X4*)(orow + d) = v;
-        }
+        for (int e = 0; e < 4; ++e) v[e] = (T)(acc[dt][4 * g + e] * inv);
+        *(LDS_AS X4*)(wb + swz_off<DP>(l32, 32 * dt + 8 * g + 4 * hh) * 2) = v;
       }
+#pragma unroll
+    for (int c = 0; c < BLK / 1024; ++c) {
+      const int byte = c * 1024 + lane * 16;
+      const int row = byte / (DP * 2), seg = (byte % (DP * 2)) / 16;
+      const X8 v = *(const LDS_AS X8*)(wb + row * DP * 2 + ((seg ^ seg_swz<DP>(row)) << 4));
+      const int q = qw_lo + row;
+      if (q < nq && seg * 8 < D) *(X8*)(O + (int64_t)q * p.son + seg * 8) = v;
     }
+  }
+  if (qrow < nq) {
     if constexpr (LSE) {
       const float le = half_sum(l_lse);
       if (hh == 0) {
