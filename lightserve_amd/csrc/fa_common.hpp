@@ -357,4 +357,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n > 0 ? n : 0, 0x00020000);
 }
 
+// Buffer accesses as device functions (the host compilation pass then
+// never meets the builtins inside a kernel's lambdas): a 16-byte-per-lane
+// direct global -> LDS load, and 16- / 4-byte stores (lanes whose offset
+// falls outside the descriptor are dropped).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, LDS_AS void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void store16(u32x4 v, __amdgpu_buffer_rsrc_t rs, int voff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, voff, 0, 0);
+}
+__device__ __forceinline__ void store4(float v, __amdgpu_buffer_rsrc_t rs, int voff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, voff, 0, 0);
+}
+
 }  // namespace lsfa

@@ -42,6 +42,8 @@
 // LDS tile is the same as for contiguous K/V. Block ids outside
 // [0, num_blocks) read as zeros.
 #include "fa_common.hpp"
+#include <atomic>
+#include <type_traits>
 
 namespace lsfa {
 
@@ -542,6 +544,541 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   }
 }
 
+// Items one persistent forward workgroup may take (its LDS item table).
+constexpr int kPersistMaxItems = 64;
+
+// Persistent dense forward: one 8-wave workgroup per CU walks a fixed list
+// of (batch, head, 256-row query tile) items, so the per-workgroup start
+// (Q rows, the first K/V tiles, the first score tile) overlaps the previous
+// item's work instead of idling the CU. The K/V tiles of consecutive items
+// form one stream through the double buffer: during an item's last step the
+// next item's first K and V tiles load and its first score tile is computed.
+// Each wave's next Q rows wait in its own LDS region (loaded during the
+// item's first step), which also stages the wave's O rows on the way out.
+// Items: the launch's (b, h, tile) list in map_tile's order; workgroup u of
+// the PU on XCD x takes, from XCD x's share, positions i PU + u (i even) and
+// i PU + PU - 1 - u (i odd), so heavy and light causal tiles pair up.
+// Requires (host-checked): dense, 8-wave shapes, Nk > 64, Nk >= Nq when
+// causal (every item has at least two key tiles), total items % 8 == 0.
+template <typename T, int DP, bool CAUSAL, bool LSE>
+__global__ __launch_bounds__(512, 1) void fa_fwd_persist_kernel(const FwdParams p) {
+  using X8 = typename VecT<T>::x8;
+  using X4 = typename VecT<T>::x4;
+  constexpr int NW = 8, BM = NW * 32, BN = 64;
+  constexpr int TILE = BN * DP;              // elements of one K or V tile
+  constexpr int LDI = TILE * 2 / 1024 / NW;  // 1 KB loads per wave per tile
+  constexpr int LDC = 2 * LDI;               // issued by waves 4-7 only
+  constexpr int KSTEPS = DP / 16, DT = DP / 32, KB = BN / 32;
+  constexpr int QB = 32 * DP * 2;  // bytes of one wave's 32 rows of Q or O
+  constexpr int QC = QB / 1024;
+  static_assert(LDI >= 1 && QC >= 1, "tile too small for the workgroup");
+
+  // K0 K1 V0 V1 | each wave's Q / O rows | the workgroup's item table
+  __shared__ __attribute__((aligned(1024))) char sm_raw[4 * TILE * 2 + NW * QB + kPersistMaxItems * 64];
+  LDS_AS char* smb = (LDS_AS char*)sm_raw;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hh = lane >> 5;
+  const bool loads = wave >= NW / 2;
+  const int lw = wave & (NW / 2 - 1);
+  const int nq = p.Nq, nk = p.Nk, off = nk - nq, D = p.D;
+  const float sl2 = p.scale_log2;
+  LDS_AS char* qst = smb + 4 * TILE * 2 + wave * QB;
+  // Arguments used only when an item starts or ends are re-read from the
+  // kernel argument segment there (scalar loads through an opaque pointer),
+  // instead of occupying scalar registers across the whole loop.
+  typedef const __attribute__((address_space(4))) FwdParams* KArgs;
+  auto kargs = [&]() __attribute__((always_inline)) -> KArgs {
+    KArgs pk = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(pk));
+    return pk;
+  };
+
+  // The workgroup's items, in order: item i is position j = i PU + u (i
+  // even) or i PU + PU - 1 - u (i odd) of XCD x's share of the launch's
+  // (b, h, tile) list in map_tile's order. Lane i of wave 0 decodes item i
+  // into a 64-byte LDS record {b, h, q0, key tiles | K, V, Q, O, L head
+  // pointers} once, before the loop; nt = 0 past the last item.
+  struct Item {
+    int b, h, q0, nt;
+    const T* k;
+    const T* v;
+  };
+  LDS_AS char* itab = smb + 4 * TILE * 2 + NW * QB;
+  if (wave == 0) {
+    const int xcd = blockIdx.x & 7, u = blockIdx.x >> 3, PU = gridDim.x >> 3;
+    const int nqt = p.num_q_tiles, BH = p.B * p.Hq, T8 = (nqt * BH) >> 3;
+    const int hg = max(p.heads_per_group, 1);
+    const int i = lane;
+    const int j = i * PU + ((i & 1) ? PU - 1 - u : u);
+    u32x4 r0 = {0u, 0u, 0u, 0u};
+    const T *kh = nullptr, *vh = nullptr, *qh = nullptr, *oh = nullptr;
+    const float* lh = nullptr;
+    if (i < kPersistMaxItems && j < T8) {
+      const int W = xcd * T8 + j;
+      const int g0 = (W / (hg * nqt)) * hg;
+      const int gh = min(hg, BH - g0);
+      const int rr = W - g0 * nqt;
+      const int level = rr / gh;
+      const int bh = g0 + (rr - level * gh);
+      const int qt = CAUSAL ? nqt - 1 - level : level;
+      const int b = bh / p.Hq, h = bh - b * p.Hq, hk = h / (p.Hq / p.Hkv);
+      const int q0 = qt * BM;
+      const int kv_end = CAUSAL ? min(nk, q0 + BM + off) : nk;
+      r0 = u32x4{(uint32_t)b, (uint32_t)h, (uint32_t)q0, (uint32_t)((kv_end + BN - 1) / BN)};
+      kh = (const T*)p.k + (int64_t)b * p.skb + (int64_t)hk * p.skh;
+      vh = (const T*)p.v + (int64_t)b * p.svb + (int64_t)hk * p.svh;
+      qh = (const T*)p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
+      oh = (const T*)p.o + (int64_t)b * p.sob + (int64_t)h * p.soh;
+      if (LSE) lh = p.lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
+    }
+    if (i < kPersistMaxItems) {
+      LDS_AS char* rec = itab + i * 64;
+      *(LDS_AS u32x4*)rec = r0;
+      *(LDS_AS uint64_t*)(rec + 16) = (uint64_t)kh;
+      *(LDS_AS uint64_t*)(rec + 24) = (uint64_t)vh;
+      *(LDS_AS uint64_t*)(rec + 32) = (uint64_t)qh;
+      *(LDS_AS uint64_t*)(rec + 40) = (uint64_t)oh;
+      *(LDS_AS uint64_t*)(rec + 48) = (uint64_t)lh;
+    }
+  }
+  __syncthreads();
+  // Scalar copies of an item record's fields (uniform LDS reads).
+  auto rec_int = [&](int i, int f) __attribute__((always_inline)) -> int {
+    return __builtin_amdgcn_readfirstlane(*(const LDS_AS int*)(itab + i * 64 + 4 * f));
+  };
+  auto rec_ptr = [&](int i, int off) __attribute__((always_inline)) -> const void* {
+    const uint64_t v = *(const LDS_AS uint64_t*)(itab + i * 64 + off);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const void*)(((uint64_t)hi << 32) | lo);
+  };
+  auto item_at = [&](int i) __attribute__((always_inline)) -> Item {
+    Item it{0, 0, 0, 0, nullptr, nullptr};
+    if (i >= kPersistMaxItems) return it;
+    it.b = rec_int(i, 0);
+    it.h = rec_int(i, 1);
+    it.q0 = rec_int(i, 2);
+    it.nt = rec_int(i, 3);
+    it.k = (const T*)rec_ptr(i, 16);
+    it.v = (const T*)rec_ptr(i, 24);
+    return it;
+  };
+
+  // K/V tile loads (waves 4-7, two chunk groups each; see fa_fwd_kernel).
+  int kvo[LDC], vvo[LDC];
+#pragma unroll
+  for (int c = 0; c < LDC; ++c) {
+    const int byte = (lw * LDC + c) * 1024 + lane * 16;
+    const int row = byte / (DP * 2);
+    const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+    kvo[c] = seg * 8 < D ? (int)(row * p.skn * 2) + seg * 16 : (int)0x80000000;
+    vvo[c] = seg * 8 < D ? (int)(row * p.svn * 2) + seg * 16 : (int)0x80000000;
+  }
+  // This wave's 32 Q rows of an item into its LDS region (row-major,
+  // swizzled; rows past nq and columns past D read as zero).
+  auto q_load = [&](int i, const Item& it) __attribute__((always_inline)) {
+    const int r0 = it.q0 + 32 * wave;
+    const KArgs pk = kargs();
+    const int64_t sqn = pk->sqn;
+    const T* src = (const T*)rec_ptr(i, 32) + (int64_t)r0 * sqn;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(src, (int)(min(nq - r0, 32) * sqn * 2));
+    int ln = lane;  // opaque: the offsets below are recomputed here, not held across the loop
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int c = 0; c < QC; ++c) {
+      const int byte = c * 1024 + ln * 16;
+      const int row = byte / (DP * 2);
+      const int seg = ((byte % (DP * 2)) / 16) ^ seg_swz<DP>(row);
+      const int vo = seg * 8 < D ? (int)(row * sqn * 2) + seg * 16 : (int)0x80000000;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(qst + c * 1024), 16, vo, 0, 0, 0);
+    }
+  };
+  X8 qreg[KSTEPS];
+  auto q_read = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      u32x4 raw = *(const LDS_AS u32x4*)(qst + swz_off<DP>(l32, 16 * kk + 8 * hh) * 2);
+      if (p.neg_q) raw ^= 0x80008000u;
+      qreg[kk] = __builtin_bit_cast(X8, raw);
+    }
+  };
+
+  int koff[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) koff[kk] = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
+  const int tr_row = 4 * hh + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int voff[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    voff[dt][0] = swz_off<DP>(tr_row, 32 * dt + tr_col) * 2;
+    voff[dt][1] = swz_off<DP>(tr_row + 8, 32 * dt + tr_col) * 2;
+  }
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+  float m_run = -1e30f, l_run = 0.f, l_lse = 0.f;
+  const float kTileSumMax = __builtin_exp2f(kMaxLog2P<T>);
+  auto kbuf = [&](int t) __attribute__((always_inline)) { return (const LDS_AS char*)smb + (t & 1) * TILE * 2; };
+  auto vbuf = [&](int t) __attribute__((always_inline)) { return (const LDS_AS char*)smb + (2 + (t & 1)) * TILE * 2; };
+
+  constexpr int kReadAhead = 4;
+  auto scores = [&](const LDS_AS char* Ks, f32x16* s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) s[kb] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const X8 a = *(const LDS_AS X8*)(Ks + kb * 32 * DP * 2 + koff[kk]);
+        s[kb] = mfma32(a, qreg[kk], s[kb]);
+      }
+    }
+    constexpr int NM = KSTEPS * KB;
+#pragma unroll
+    for (int i = 0; i < kReadAhead; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (j + kReadAhead < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+  auto row_max = [&](const f32x16* s) __attribute__((always_inline)) -> float {
+    float mx = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+    mx = half_max(mx);
+    return mx == -INFINITY ? -INFINITY : mx * sl2;
+  };
+  auto softmax = [&](const f32x16* s, X8* pb) __attribute__((always_inline)) -> float2 {
+    constexpr bool kF16 = std::is_same<T, _Float16>::value;
+    const float neg_m = -m_run;
+    float rs[4] = {-0.f, -0.f, -0.f, -0.f}, re[4] = {-0.f, -0.f, -0.f, -0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      f32x16 pp;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        pp[i] = fast_exp2(fmaf(s[kb][i], sl2, neg_m));
+        if constexpr (LSE || kF16) re[i & 3] += pp[i];
+      }
+      pb[2 * kb] = pack8<T>(pp, 0);
+      pb[2 * kb + 1] = pack8<T>(pp, 8);
+      if constexpr (!kF16) {
+        sum8_into(pb[2 * kb], rs);
+        sum8_into(pb[2 * kb + 1], rs);
+      }
+    }
+    float2 r;
+    r.y = (LSE || kF16) ? (re[0] + re[1]) + (re[2] + re[3]) : 0.f;
+    r.x = kF16 ? r.y : (rs[0] + rs[1]) + (rs[2] + rs[3]);
+    return r;
+  };
+  auto softmax_checked = [&](const f32x16* s, X8* pb) __attribute__((always_inline)) {
+    float2 ts = softmax(s, pb);
+    if (__builtin_amdgcn_ballot_w64(ts.x > kTileSumMax) != 0) {
+      const float mx = row_max(s);
+      if (__builtin_amdgcn_ballot_w64(mx > m_run) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = fast_exp2(m_run - m_new);
+        l_run *= alpha;
+        if constexpr (LSE) l_lse *= alpha;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+      }
+      ts = softmax(s, pb);
+    }
+    l_run += ts.x;
+    if constexpr (LSE) l_lse += ts.y;
+  };
+  auto pv = [&](const LDS_AS char* Vs, const X8* pb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int ks = 0; ks < 2 * KB; ++ks) {
+        const LDS_AS char* base = Vs + ks * 16 * DP * 2;
+        const X8 a = cat4<X8, X4>(lds_read_tr((const LDS_AS T*)(base + voff[dt][0])),
+                                  lds_read_tr((const LDS_AS T*)(base + voff[dt][1])));
+        acc[dt] = mfma32(a, pb[ks], acc[dt]);
+      }
+    }
+    constexpr int NM = DT * 2 * KB;
+#pragma unroll
+    for (int i = 0; i < kReadAhead; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (j + kReadAhead < NM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+  // qlo: the first of this wave's 32 query rows in the item.
+  auto wave_sees = [&](int qlo, int j) __attribute__((always_inline)) { return !CAUSAL || j * BN <= qlo + 31 + off; };
+  auto mask_tile = [&](int qlo, int j, f32x16* s) __attribute__((always_inline)) {
+    const int kbase = j * BN;
+    if ((kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > qlo + off)) {
+      asm volatile("" ::: "memory");
+      int lim = nk - 1 - kbase - 4 * hh;
+      if (CAUSAL) lim = min(lim, qlo + l32 + off - kbase - 4 * hh);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          s[kb][i] = 32 * kb + 8 * (i >> 2) + (i & 3) > lim ? -INFINITY : s[kb][i];
+    }
+  };
+  // O (and L) of an item: through this wave's LDS region, four whole rows
+  // per store instruction.
+  // An item ends in two parts. finish_stage (its last step): O / l goes
+  // into this wave's LDS region as the input dtype, and L into a register.
+  // finish_store (the start of the next step, so that the global stores
+  // complete under that step's work): the rows leave LDS row-major, four
+  // whole rows per store instruction, through buffer stores clipped to the
+  // rows that exist (rows past nq and columns past D are dropped).
+  float lpend = 0.f;
+  int st_item = 0, st_qlo = 0;
+  bool st_due = false;
+  auto finish_stage = [&](int qlo) __attribute__((always_inline)) {
+    const float lt = half_sum(l_run);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    // Lane-dependent offsets come from an opaque copy of the lane id, so
+    // that the compiler computes them here instead of keeping them in
+    // registers across the whole loop.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int l32o = ln & 31, hho = ln >> 5;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        X4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (T)(acc[dt][4 * g + e] * inv);
+        *(LDS_AS X4*)(qst + swz_off<DP>(l32o, 32 * dt + 8 * g + 4 * hho) * 2) = v;
+      }
+    if constexpr (LSE) {
+      const float le = half_sum(l_lse);
+      lpend = le > 0.f ? (m_run + __log2f(le)) * kLn2 : -INFINITY;
+    }
+  };
+  auto finish_store = [&]() __attribute__((always_inline)) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const KArgs pk = kargs();
+    const int64_t son = pk->son;
+    const int rows = min(nq - st_qlo, 32);
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc((const T*)rec_ptr(st_item, 40) + (int64_t)st_qlo * son, (int)(rows * son * 2));
+#pragma unroll
+    for (int c = 0; c < QC; ++c) {
+      const int byte = c * 1024 + ln * 16;
+      const int row = byte / (DP * 2), seg = (byte % (DP * 2)) / 16;
+      const u32x4 v = *(const LDS_AS u32x4*)(qst + row * DP * 2 + ((seg ^ seg_swz<DP>(row)) << 4));
+      store16(v, rs, seg * 8 < D ? (int)(row * son * 2) + seg * 16 : (int)0x80000000);
+    }
+    if constexpr (LSE) {
+      const int64_t sln = pk->sln;
+      const __amdgpu_buffer_rsrc_t lr = tile_rsrc((const float*)rec_ptr(st_item, 48) + (int64_t)st_qlo * sln, (int)(rows * sln * 4));
+      store4(lpend, lr, (ln >> 5) == 0 ? (int)((ln & 31) * sln * 4) : (int)0x80000000);
+    }
+  };
+
+  int item = 0;
+  Item cur = item_at(0);
+  if (cur.nt == 0) return;  // uniform, before any barrier
+  Item nxt = item_at(1);
+  int qlo = cur.q0 + 32 * wave;
+  // Load cursors of the K and V streams: the next tile's first row, the key
+  // rows from there to the sequence end (the last tile's descriptor is
+  // clipped to them), and the tiles left in the item the cursor is in. A
+  // cursor that runs out moves to the next item (items have at least two
+  // tiles, and K runs at most two tiles ahead of the computation, so that
+  // is always nxt).
+  const int64_t kstep = (int64_t)BN * p.skn, vstep = (int64_t)BN * p.svn;
+  const int krow2 = (int)(p.skn * 2), vrow2 = (int)(p.svn * 2);
+  const T* kp = cur.k;
+  const T* vp = cur.v;
+  int krows = nk, vrows = nk;  // key rows from the cursor's tile to the sequence end
+  int kleft = cur.nt, vleft = cur.nt;
+  auto k_next = [&](int buf) __attribute__((always_inline)) {
+    if (loads) {
+      const __amdgpu_buffer_rsrc_t rs = tile_rsrc(kp, min(krows, BN) * krow2);
+      LDS_AS char* dst = smb + buf * TILE * 2;
+#pragma unroll
+      for (int c = 0; c < LDC; ++c) dma16(rs, (LDS_AS void*)(dst + (lw * LDC + c) * 1024), kvo[c]);
+    }
+    kp += kstep;
+    krows -= BN;
+    --kleft;
+  };
+  auto v_next = [&](int buf) __attribute__((always_inline)) {
+    if (loads) {
+      const __amdgpu_buffer_rsrc_t rs = tile_rsrc(vp, min(vrows, BN) * vrow2);
+      LDS_AS char* dst = smb + buf * TILE * 2;
+#pragma unroll
+      for (int c = 0; c < LDC; ++c) dma16(rs, (LDS_AS void*)(dst + (lw * LDC + c) * 1024), vvo[c]);
+    }
+    vp += vstep;
+    vrows -= BN;
+    --vleft;
+  };
+  // A cursor that has run out moves to the next item first.
+  auto k_issue = [&](int buf) __attribute__((always_inline)) {
+    if (kleft == 0) {
+      if (nxt.nt == 0) return;
+      kp = nxt.k;
+      krows = nk;
+      kleft = nxt.nt;
+    }
+    k_next(buf);
+  };
+  auto v_issue = [&](int buf) __attribute__((always_inline)) {
+    if (vleft == 0) {
+      if (nxt.nt == 0) return;
+      vp = nxt.v;
+      vrows = nk;
+      vleft = nxt.nt;
+    }
+    v_next(buf);
+  };
+  q_load(0, cur);
+  k_issue(0);
+  v_issue(2);
+  k_issue(1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  q_read();
+  f32x16 s0[KB], s1[KB];
+  if (wave_sees(qlo, 0)) {
+    scores(kbuf(0), s0);
+    mask_tile(qlo, 0, s0);
+    m_run = fmaxf(row_max(s0), -1e30f);
+  }
+  // The next item's Q rows load during the first step (the region was just read).
+  bool q_due = nxt.nt > 0;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __syncthreads();  // K buffer 0 is refilled by the first step
+  int t = 0;
+  // Steps: tile t of the current item (in buffer PAR, the parity of its
+  // position in the workgroup's stream) is finished and the stream's next
+  // tile is scored.
+  // A step in the middle of an item (1 <= t <= nt - 3): the K and V
+  // cursors stay inside the item and nothing changes hands, so the step
+  // carries no item bookkeeping.
+  auto fast_step = [&](auto par_c, f32x16* sc, f32x16* sn) __attribute__((always_inline)) {
+    constexpr int PAR = decltype(par_c)::value;
+    k_next(PAR);
+    if (wave_sees(qlo, t + 1)) {
+      scores(kbuf(PAR ^ 1), sn);
+      mask_tile(qlo, t + 1, sn);
+    }
+    v_next(2 + (PAR ^ 1));
+    if (wave_sees(qlo, t)) {
+      X8 pb[2 * KB];
+      softmax_checked(sc, pb);
+      pv(vbuf(PAR), pb);
+    }
+    ++t;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  };
+  // Any other step (an item's first, next-to-last and last): cursors may
+  // move to the next item, the next item's Q rows load (first step) or come
+  // into registers and its first score tile is computed (last step), and
+  // the item is finished. Returns false after the workgroup's last item.
+  auto slow_step = [&](auto par_c, f32x16* sc, f32x16* sn) __attribute__((always_inline)) -> bool {
+    constexpr int PAR = decltype(par_c)::value;
+    const bool last = t + 1 == cur.nt;
+    k_issue(PAR);  // K tile two ahead in the stream
+    if (st_due) {  // the previous item's O and L rows leave
+      finish_store();
+      st_due = false;
+    }
+    if (q_due) {  // the next item's Q rows load into the region just read
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      q_load(item + 1, nxt);
+      q_due = false;
+    }
+    const int jn = last ? 0 : t + 1;
+    const bool more = !last || nxt.nt > 0;
+    const int qlo_n = last ? nxt.q0 + 32 * wave : qlo;
+    if (last && more) q_read();
+    const bool s_next = more && wave_sees(qlo_n, jn);
+    if (s_next) {
+      scores(kbuf(PAR ^ 1), sn);
+      mask_tile(qlo_n, jn, sn);
+    }
+    v_issue(2 + (PAR ^ 1));
+    if (wave_sees(qlo, t)) {
+      X8 pb[2 * KB];
+      softmax_checked(sc, pb);
+      pv(vbuf(PAR), pb);
+    }
+    if (last) {
+      const float m_next = s_next ? fmaxf(row_max(sn), -1e30f) : -1e30f;
+      finish_stage(qlo);
+      st_item = item;
+      st_qlo = qlo;
+      st_due = true;
+      m_run = m_next;
+      l_run = 0.f;
+      l_lse = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+      ++item;
+      cur = nxt;
+      qlo = cur.q0 + 32 * wave;
+      t = 0;
+      if (cur.nt > 0) {
+        nxt = item_at(item + 1);
+        q_due = nxt.nt > 0;
+      }
+    } else {
+      ++t;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    return cur.nt > 0;
+  };
+  // Two general steps, then middle-of-item steps in pairs while the item
+  // has them (the pair keeps the buffer parity a compile-time constant).
+  for (;;) {
+    if (!slow_step(std::integral_constant<int, 0>{}, s0, s1)) break;
+    if (!slow_step(std::integral_constant<int, 1>{}, s1, s0)) break;
+    while (t >= 1 && t + 3 < cur.nt) {
+      fast_step(std::integral_constant<int, 0>{}, s0, s1);
+      fast_step(std::integral_constant<int, 1>{}, s1, s0);
+    }
+  }
+  if (st_due) finish_store();
+}
+
+template <typename T, int DP, bool CAUSAL>
+static hipError_t launch_fwd_persist(FwdParams p, int grid, hipStream_t s) {
+  p.num_q_tiles = (p.Nq + 255) / 256;
+  if (p.lse != nullptr)
+    hipLaunchKernelGGL((fa_fwd_persist_kernel<T, DP, CAUSAL, true>), dim3(grid), dim3(512), 0, s, p);
+  else
+    hipLaunchKernelGGL((fa_fwd_persist_kernel<T, DP, CAUSAL, false>), dim3(grid), dim3(512), 0, s, p);
+  return hipGetLastError();
+}
+
+// Compute units of the current device (cached per device id; 0 if unknown).
+static int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = -1;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n > 0 ? n : 0;
+}
+
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED, int NW>
 static hipError_t launch_fwd_nw(FwdParams p, hipStream_t s) {
   p.num_q_tiles = (p.Nq + NW * 32 - 1) / (NW * 32);
@@ -559,10 +1096,23 @@ static hipError_t launch_fwd_nw(FwdParams p, hipStream_t s) {
 // varlen batches (packed or paged K/V) of up to 64 sequences (the
 // longest-first ranking) with runs of at least 512 queries (config 5,
 // 512-query chunks over 2.4k-7.3k keys: -5%).
+// Dense 8-wave launches with more items than CUs run persistent (one
+// workgroup per CU streaming its items; bit-identical outputs, -2.4% at the
+// config-3 shape, -0.5 to -1.1% at the other dense shapes measured) when
+// every item has at least two key tiles (Nk > 64, and Nk >= Nq if causal),
+// the item count splits evenly over the 8 XCDs and no workgroup takes more
+// than kPersistMaxItems items.
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED = false>
 static hipError_t launch_fwd(const FwdParams& p, hipStream_t s) {
   if constexpr (!VARLEN && !PAGED && DP >= 64) {
-    if (p.Nq >= 4096) return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);
+    if (p.Nq >= 4096) {
+      const int total = ((p.Nq + 255) / 256) * p.B * p.Hq;
+      const int grid = (cu_count() / 8) * 8;
+      if (grid >= 8 && total > grid && total % 8 == 0 && (total / 8 + grid / 8 - 1) / (grid / 8) <= kPersistMaxItems &&
+          p.Nk > 64 && (!CAUSAL || p.Nk >= p.Nq))
+        return launch_fwd_persist<T, DP, CAUSAL>(p, grid, s);
+      return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);
+    }
   }
   if constexpr (VARLEN && DP >= 64) {
     if (p.B <= 64 && p.Nq >= 512) return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);

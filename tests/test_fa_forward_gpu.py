@@ -253,3 +253,48 @@ def test_wide_workgroups(gpu, B, H, N, D, causal, dtype):
     o_ref, lse_ref = _oracle_gpu_chunked(q.float(), k.float(), v.float(), causal, heads_per_chunk=1)
     assert_gate(o.float(), o_ref, f"wide {N} o")
     assert_lse(lse, lse_ref, f"wide {N}")
+
+
+def _abi_fwd(q, k, v, causal, scale):
+    """Forward with L through the C ABI (Nq != Nk allowed), into NaN-filled
+    outputs so that a row the kernel never writes shows."""
+    from lightserve_amd import _lib
+    B, H, Nq, D = q.shape
+    o = torch.full_like(q, float("nan"))
+    L = torch.full((B, H, Nq), float("nan"), device=q.device, dtype=torch.float32)
+    fa = _lib.FwdArgs(q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), o=o.data_ptr(), lse=L.data_ptr(),
+                      q_stride=_lib.strides4(q), k_stride=_lib.strides4(k), v_stride=_lib.strides4(v),
+                      o_stride=_lib.strides4(o), lse_stride=_lib._i64x3(*L.stride()),
+                      cu_seqlens_q=None, cu_seqlens_k=None, dtype=_lib.TORCH_TO_LSFA[q.dtype], batch=B, heads_q=H,
+                      heads_kv=k.shape[1], seqlen_q=Nq, seqlen_k=k.shape[2], head_dim=D, causal=int(causal),
+                      sm_scale=scale, reserved=0)
+    _lib.fwd(fa, _lib.current_stream(q.device))
+    return o, L
+
+
+@pytest.mark.parametrize("B,H,Nq,Nk,D,causal,dtype,layout", [
+    (2, 16, 4200, 4200, 128, True, torch.bfloat16, "bhnd"),   # 544 items, ragged last query tile
+    (3, 24, 4096, 4096, 64, False, torch.float16, "bhnd"),    # 1152 items: 4 or 5 per workgroup
+    (2, 16, 4096, 4608, 128, True, torch.bfloat16, "bhnd"),   # Nk > Nq, bottom-right causal
+    (2, 16, 4200, 4200, 96, False, torch.bfloat16, "bhnd"),   # padded head dim
+    (2, 16, 4096, 4096, 128, True, torch.bfloat16, "bnhd"),   # rows strided by H * D
+])
+def test_persistent_forward(gpu, B, H, Nq, Nk, D, causal, dtype, layout):
+    """Dense 8-wave launches with more (b, h, 256-row tile) items than CUs run
+    one workgroup per CU that streams its items (the K/V tiles of consecutive
+    items through one double buffer, the next item's Q rows and first score
+    tile during the current item's last step, O and L stored one step late):
+    every row of every (b, h) written once and within the gate."""
+    print(f"case persistent forward {B}x{H} Nq={Nq} Nk={Nk} D={D} causal={causal} {dtype} {layout}", flush=True)
+    g = torch.Generator().manual_seed(Nq + Nk + D)
+    if layout == "bnhd":
+        q = torch.randn(B, Nq, H, D, generator=g).to(dtype).to(gpu).transpose(1, 2)
+        k, v = (torch.randn(B, Nk, H, D, generator=g).to(dtype).to(gpu).transpose(1, 2) for _ in range(2))
+    else:
+        q = torch.randn(B, H, Nq, D, generator=g).to(dtype).to(gpu)
+        k, v = (torch.randn(B, H, Nk, D, generator=g).to(dtype).to(gpu) for _ in range(2))
+    o, lse = _abi_fwd(q, k, v, causal, 1.0 / math.sqrt(D))
+    assert not torch.isnan(o).any() and not torch.isnan(lse).any(), "a row was left unwritten"
+    o_ref, lse_ref = _oracle_gpu_chunked(q.float(), k.float(), v.float(), causal, heads_per_chunk=4)
+    assert_gate(o.float(), o_ref, f"persistent {Nq}x{Nk} o")
+    assert_lse(lse, lse_ref, f"persistent {Nq}x{Nk}")
