@@ -544,8 +544,13 @@ __global__ __launch_bounds__((NW * 64), (8 / NW)) void fa_fwd_kernel(const FwdPa
   }
 }
 
-// Items one persistent forward workgroup may take (its LDS item table).
+// Items one persistent forward workgroup may take (its LDS item table), and
+// the fewest per workgroup for which the fixed split beats the hardware's
+// own dispatch of one workgroup per item (measured: 8 per workgroup -2.4%,
+// 4 per workgroup -0.5 to -1.1%, 4.5 even, 2.1 per workgroup +31%, where a
+// fixed split of so few causal items leaves a long tail).
 constexpr int kPersistMaxItems = 64;
+constexpr int kPersistMinItems = 4;
 
 // Persistent dense forward: one 8-wave workgroup per CU walks a fixed list
 // of (batch, head, 256-row query tile) items, so the per-workgroup start
@@ -1096,20 +1101,19 @@ static hipError_t launch_fwd_nw(FwdParams p, hipStream_t s) {
 // varlen batches (packed or paged K/V) of up to 64 sequences (the
 // longest-first ranking) with runs of at least 512 queries (config 5,
 // 512-query chunks over 2.4k-7.3k keys: -5%).
-// Dense 8-wave launches with more items than CUs run persistent (one
-// workgroup per CU streaming its items; bit-identical outputs, -2.4% at the
-// config-3 shape, -0.5 to -1.1% at the other dense shapes measured) when
-// every item has at least two key tiles (Nk > 64, and Nk >= Nq if causal),
-// the item count splits evenly over the 8 XCDs and no workgroup takes more
-// than kPersistMaxItems items.
+// Dense 8-wave launches with at least kPersistMinItems items per CU run
+// persistent (one workgroup per CU streaming its items; bit-identical
+// outputs) when every item has at least two key tiles (Nk > 64, and
+// Nk >= Nq if causal), the item count splits evenly over the 8 XCDs and no
+// workgroup takes more than kPersistMaxItems items.
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED = false>
 static hipError_t launch_fwd(const FwdParams& p, hipStream_t s) {
   if constexpr (!VARLEN && !PAGED && DP >= 64) {
     if (p.Nq >= 4096) {
       const int total = ((p.Nq + 255) / 256) * p.B * p.Hq;
       const int grid = (cu_count() / 8) * 8;
-      if (grid >= 8 && total > grid && total % 8 == 0 && (total / 8 + grid / 8 - 1) / (grid / 8) <= kPersistMaxItems &&
-          p.Nk > 64 && (!CAUSAL || p.Nk >= p.Nq))
+      if (grid >= 8 && total >= kPersistMinItems * grid && total % 8 == 0 &&
+          (total / 8 + grid / 8 - 1) / (grid / 8) <= kPersistMaxItems && p.Nk > 64 && (!CAUSAL || p.Nk >= p.Nq))
         return launch_fwd_persist<T, DP, CAUSAL>(p, grid, s);
       return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);
     }

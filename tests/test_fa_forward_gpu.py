@@ -273,15 +273,16 @@ def _abi_fwd(q, k, v, causal, scale):
 
 
 @pytest.mark.parametrize("B,H,Nq,Nk,D,causal,dtype,layout", [
-    (2, 16, 4200, 4200, 128, True, torch.bfloat16, "bhnd"),   # 544 items, ragged last query tile
+    (4, 16, 4200, 4200, 128, True, torch.bfloat16, "bhnd"),   # 1088 items, ragged last query tile
     (3, 24, 4096, 4096, 64, False, torch.float16, "bhnd"),    # 1152 items: 4 or 5 per workgroup
-    (2, 16, 4096, 4608, 128, True, torch.bfloat16, "bhnd"),   # Nk > Nq, bottom-right causal
-    (2, 16, 4200, 4200, 96, False, torch.bfloat16, "bhnd"),   # padded head dim
-    (2, 16, 4096, 4096, 128, True, torch.bfloat16, "bnhd"),   # rows strided by H * D
+    (4, 16, 4096, 4608, 128, True, torch.bfloat16, "bhnd"),   # Nk > Nq, bottom-right causal
+    (4, 16, 4200, 4200, 96, False, torch.bfloat16, "bhnd"),   # padded head dim
+    (4, 16, 4096, 4096, 128, True, torch.bfloat16, "bnhd"),   # rows strided by H * D
+    (2, 16, 4200, 4200, 128, True, torch.bfloat16, "bhnd"),   # 544 items: too few, per-item kernel
 ])
 def test_persistent_forward(gpu, B, H, Nq, Nk, D, causal, dtype, layout):
-    """Dense 8-wave launches with more (b, h, 256-row tile) items than CUs run
-    one workgroup per CU that streams its items (the K/V tiles of consecutive
+    """Dense 8-wave launches with at least four (b, h, 256-row tile) items per
+    CU (1024 on MI355X) run one workgroup per CU that streams its items (the K/V tiles of consecutive
     items through one double buffer, the next item's Q rows and first score
     tile during the current item's last step, O and L stored one step late):
     every row of every (b, h) written once and within the gate."""
