@@ -113,6 +113,24 @@ def measured_traffic(kernel, workload):
     return None
 
 
+def fwd_kernel_name(B, H, Nq, Nk, D, causal, dtype):
+    """The forward kernel the library launches for a dense call (the host
+    dispatch of lightserve_amd/csrc/fa_fwd.hip): the persistent 8-wave kernel
+    from 4096 queries at head dims above 32 when every CU gets at least four
+    (b, h, 256-row tile) items (at most 64) that split evenly over the 8 XCDs
+    and every item has two key tiles; else the one-workgroup-per-item
+    kernel."""
+    import torch
+    if dtype == torch.float32 or D <= 32 or Nq < 4096:
+        return "fa_fwd_kernel"
+    total = -(-Nq // 256) * B * H
+    grid = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
+    if (grid >= 8 and total >= 4 * grid and total % 8 == 0 and -(-(total // 8) // (grid // 8)) <= 64
+            and Nk > 64 and (not causal or Nk >= Nq)):
+        return "fa_fwd_persist_kernel"
+    return "fa_fwd_kernel"
+
+
 def check_parity(cfg, inp, outs, slices=None):
     """Oracle check of every (batch, head) slice (fp32 oracle on the GPU), or
     of the given (batch, head) slices.
@@ -1171,7 +1189,8 @@ def main():
     # reported beside the default; its dQ GEMM moves dS once, so it is priced
     # against HBM bandwidth (algorithmic bytes: the visible dS entries, 2
     # bytes each, plus K and dQ).
-    kernels = [{"kernel": "fa_fwd_kernel", "bound": "mfma", "flops_per_launch": f_fwd,
+    fwd_name = fwd_kernel_name(*q.shape[:3], k.shape[2], q.shape[3], inp["causal"], q.dtype)
+    kernels = [{"kernel": fwd_name, "bound": "mfma", "flops_per_launch": f_fwd,
                 "mfma_flops_per_launch": f_fwd, "avg_launch_ms": fwd_avg}]
     stored_ds = None
     if bwd is not None:
