@@ -353,6 +353,10 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
 // contiguous memory. Keys at or past nk are stored as zero, masked (causal)
 // entries are zero already.
 // ---------------------------------------------------------------------------
+// s_waitcnt immediate: wait until at most n vector-memory operations of the
+// wave are outstanding (expcnt and lgkmcnt left at their maxima).
+constexpr int vmcnt_enc(int n) { return 0x0F70 | (n & 15) | (((n >> 4) & 3) << 14); }
+
 template <typename T, int DP, bool CAUSAL, bool DS, bool GQA = false, bool VARLEN = false>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) {
   using X8 = typename VecT<T>::x8;
@@ -361,7 +365,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
   constexpr int KSTEPS = DP / 16, DT = DP / 32;
   constexpr int R_B = BMQ * DP * 2;     // bytes of a row-major Q (or dO) tile
   constexpr int RS_B = 2 * R_B + 1024;  // one stage: Q | dO | 64 L*log2e | 64 -delta, 1 KB aligned
-  constexpr int LDS_B = NST * RS_B;
+  constexpr int KV_B = 4 * R_B;        // the prologue's K / V rows, from stage 2 on
+  constexpr int LDS_B = (NST - 1) * RS_B + KV_B;
   constexpr int CR = 2 * R_B / 1024 / NW;  // 1 KB chunks per wave per tile (Q|dO)
   static_assert(CR >= 1, "tile too small for the workgroup");
   static_assert(LDS_B <= 160 * 1024, "LDS budget");
@@ -461,23 +466,76 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
                                                0);
     }
   };
-  // The first three tiles go in flight before the K / V register loads.
+  // Prologue only: the rows of tile tt (an empty descriptor past the last
+  // tile, whose loads then write zeros to a stage read by no one), and the
+  // tile's L*log2e / -delta pairs (wave 0).
+  auto load_rows_pro = [&](int tt, int stage) {
+    const bool live = tt < n_all;
+    const int g = live ? head_of(tt) : 0;
+    const int q0 = live ? (t_begin + tt - g * n_t) * BMQ : 0;
+    const int rows = live ? min(nq - q0, BMQ) : 0;
+    const int64_t sn = w_hi ? p.sdon : p.sqn;
+    const T* src = w_hi ? dO + (int64_t)g * p.sdoh : Q + (int64_t)g * p.sqh;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(src + (int64_t)q0 * sn, (int)(rows * sn * 2));
+    LDS_AS char* base = sm + stage * RS_B + (w_hi ? R_B : 0);
 #pragma unroll
-  for (int i = 0; i < NST; ++i)
-    if (i < n_all) load_tile(i, i, rvo);
+    for (int i = 0; i < CR; ++i) dma16(rs, (LDS_AS void*)(base + ((wave % (NW / 2)) * CR + i) * 1024), rvo[i]);
+  };
+  auto load_ld_pro = [&](int tt, int stage) {
+    if (wave == 0 && lane < BMQ * 8 / 16) {
+      const int g = head_of(tt);
+      const int q0 = (t_begin + tt - g * n_t) * BMQ;
+      const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(LD + (int64_t)g * p.sldh + 2 * (int64_t)q0, BMQ * 8);
+      dma16(lrs, (LDS_AS void*)(sm + stage * RS_B + 2 * R_B), lane * 16);
+    }
+  };
+  // Prologue. The first tile goes into stage 0, the workgroup's 128 K and
+  // 128 V rows into the space from stage 2 on, then the second tile into
+  // stage 1, all by direct 1 KB loads of whole rows (each 128-byte line is
+  // requested once; per-lane register loads of 16 bytes from 32 rows
+  // touched every line four times and took most of the prologue). Wave w
+  // loads K (w < 2) or V (w >= 2) rows 64 (w % 2) .. +63, swizzled like a Q
+  // tile; rows at or past nk and columns at or past D read as zero. The
+  // first scores wait for the first tile and K / V only; the second tile
+  // lands under them.
+  if (n_all > 0) load_tile(0, 0, rvo);
+  if (1 < n_all) load_ld_pro(1, 1);
+  {
+    const int r0 = 64 * (wave % 2);
+    const int rows = max(0, min(nk - k0 - r0, BMQ));
+    const int64_t sn = w_hi ? p.svn : p.skn;
+    const T* src = (w_hi ? V : K) + (int64_t)(k0 + r0) * sn;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(src, (int)(rows * sn * 2));
+    LDS_AS char* base = sm + (NST - 1) * RS_B + (w_hi ? 2 : 0) * R_B + (wave % 2) * R_B;
+#pragma unroll
+    for (int i = 0; i < R_B / 1024; ++i) dma16(rs, (LDS_AS void*)(base + i * 1024), row_voff(i, sn));
+  }
+  // Issued on every path (no branch from here to the wait, so that the
+  // count below is exact): the wave's CR row loads of the second tile.
+  load_rows_pro(1, 1);
+  // The first tile and K / V have landed once at most those CR loads are
+  // outstanding (a wave's loads retire in order); a plain barrier, since
+  // __syncthreads() would also wait for the second tile.
+  __builtin_amdgcn_s_waitcnt(vmcnt_enc(CR));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 
   // K and V rows of this lane's key as B operands: columns 16kk + 8hh .. +7.
   X8 kreg[KSTEPS], vreg[KSTEPS];
+  {
+    const LDS_AS char* kr = sm + (NST - 1) * RS_B + (kb / 2) * R_B + 32 * (kb % 2) * DP * 2;
 #pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) {
-    const int col = 16 * kk + 8 * hh;
-    u32x4 kr = {0, 0, 0, 0}, vr = {0, 0, 0, 0};
-    if (kcol < nk && col < D) {
-      kr = ldg16(K + (int64_t)kcol * p.skn + col);
-      vr = ldg16(V + (int64_t)kcol * p.svn + col);
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const int o = swz_off<DP>(l32, 16 * kk + 8 * hh) * 2;
+      // straight into accumulation registers, where the loop's MFMAs read
+      // them as B operands (a VGPR result would be parked there and copied
+      // back before every use)
+      const uint32_t ka = (uint32_t)(uintptr_t)(kr + o), va = (uint32_t)(uintptr_t)(kr + 2 * R_B + o);
+      asm volatile("ds_read_b128 %0, %1" : "=a"(kreg[kk]) : "v"(ka) : "memory");
+      asm volatile("ds_read_b128 %0, %1" : "=a"(vreg[kk]) : "v"(va) : "memory");
     }
-    kreg[kk] = __builtin_bit_cast(X8, kr);
-    vreg[kk] = __builtin_bit_cast(X8, vr);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 
   int roff[KSTEPS];
@@ -691,10 +749,13 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const BwdParams p) 
     }
   };
 
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
   f32x16 sa, da, sb, db;  // S / dP of the current and the next half
   if (n_all > 0) scores(sm, 0, sa, da);
+  // The second tile has landed and every wave holds its K / V rows; then
+  // stage 2 takes its tile (which lands by the first iteration's closing
+  // wait, one tile before its use).
+  __syncthreads();
+  if (NST - 1 < n_all) load_tile(NST - 1, NST - 1, rvo);
   // Per tile: the second half's S/dP beside the first half's softmax, the
   // first half's dV/dK; the next tile's first-half S/dP beside the second
   // half's softmax (past the last tile they read a stale stage and are
