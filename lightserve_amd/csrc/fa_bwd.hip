@@ -146,28 +146,12 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   __syncthreads();
 
   X8 qreg[KSTEPS], doreg[KSTEPS];
-  float dpart = 0.f;
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
     const int o = swz_off<DP>(32 * wave + l32, 16 * kk + 8 * hh) * 2;
     qreg[kk] = *(const LDS_AS X8*)(sm + o);
     doreg[kk] = *(const LDS_AS X8*)(sm + TB + o);
-    const X8 ov = __builtin_bit_cast(X8, oraw[kk]);
-#pragma unroll
-    for (int s = 0; s < 8; ++s) dpart += (float)doreg[kk][s] * (float)ov[s];
   }
-  const float delta = half_sum(dpart);
-  const float l2 = lraw == -INFINITY ? INFINITY : lraw * kLog2eB;  // no visible key / padding: P == 0
-  if (hh == 0) {
-    float* w = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + (qrow >> 6) * 128 + (qrow & 63);
-    w[0] = l2;
-    w[64] = -delta;
-  }
-  // dP^T - delta accumulates from -delta (this lane's query in every
-  // register), so dS = P (dP - delta) is one multiply per score.
-  f32x16 negd;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) negd[i] = -delta;
   __syncthreads();  // the K/V tiles below reuse the Q/dO buffers
 
   int kv_end = nk;
@@ -191,6 +175,31 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
     for (int c = 0; c < LDI; ++c)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LDS_AS void*)(dst + (wave * LDI + c) * 1024), 16, vo[c], 0, 0, 0);
   };
+  // The first K/V tiles load while delta is computed.
+  if (ntiles > 0) {
+    tile_load(K, p.skn, kvo, 0, 0);
+    tile_load(V, p.svn, vvo, 0, 2);
+  }
+
+  float dpart = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) {
+    const X8 ov = __builtin_bit_cast(X8, oraw[kk]);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) dpart += (float)doreg[kk][s] * (float)ov[s];
+  }
+  const float delta = half_sum(dpart);
+  const float l2 = lraw == -INFINITY ? INFINITY : lraw * kLog2eB;  // no visible key / padding: P == 0
+  if (hh == 0) {
+    float* w = p.ld + (int64_t)b * p.sldb + (int64_t)h * p.sldh + (qrow >> 6) * 128 + (qrow & 63);
+    w[0] = l2;
+    w[64] = -delta;
+  }
+  // dP^T - delta accumulates from -delta (this lane's query in every
+  // register), so dS = P (dP - delta) is one multiply per score.
+  f32x16 negd;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) negd[i] = -delta;
 
   int koff[KSTEPS];
 #pragma unroll
@@ -201,10 +210,6 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const BwdParams p) {
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
   const float sl2 = p.scale_log2;
 
-  if (ntiles > 0) {
-    tile_load(K, p.skn, kvo, 0, 0);
-    tile_load(V, p.svn, vvo, 0, 2);
-  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
