@@ -115,20 +115,45 @@ def measured_traffic(kernel, workload):
 
 def fwd_kernel_name(B, H, Nq, Nk, D, causal, dtype):
     """The forward kernel the library launches for a dense call (the host
-    dispatch of lightserve_amd/csrc/fa_fwd.hip): the persistent 8-wave kernel
-    from 4096 queries at head dims above 32 when every CU gets at least four
-    (b, h, 256-row tile) items (at most 64) that split evenly over the 8 XCDs
-    and every item has two key tiles; else the one-workgroup-per-item
-    kernel."""
+    dispatch of lightserve_amd/csrc/fa_fwd.hip, launch_fwd and
+    persist_balanced): the persistent 8-wave kernel from 4096 queries (2048
+    at head dims above 64) when every CU gets at least four (b, h, 256-row
+    tile) items (at most 64) that split evenly over the 8 XCDs, every item
+    has two key tiles and, when causal, the fixed split's largest workgroup
+    holds at most 2% more key tiles than the mean; else the
+    one-workgroup-per-item kernel."""
     import torch
-    if dtype == torch.float32 or D <= 32 or Nq < 4096:
+    dp = 32 if D <= 32 else (64 if D <= 64 else 128)
+    if dtype == torch.float32 or dp < 64 or Nq < (2048 if dp >= 128 else 4096):
         return "fa_fwd_kernel"
-    total = -(-Nq // 256) * B * H
+    nqt = -(-Nq // 256)
+    BH = B * H
+    total = nqt * BH
     grid = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
-    if (grid >= 8 and total >= 4 * grid and total % 8 == 0 and -(-(total // 8) // (grid // 8)) <= 64
+    PU, T8 = grid // 8, total // 8
+    if not (grid >= 8 and total >= 4 * grid and total % 8 == 0 and -(-T8 // PU) <= 64
             and Nk > 64 and (not causal or Nk >= Nq)):
+        return "fa_fwd_kernel"
+    if not causal:
         return "fa_fwd_persist_kernel"
-    return "fa_fwd_kernel"
+    hg = max(1, min(16, (8 << 20) // (Nk * dp * 4)))
+    off, tot, worst = Nk - Nq, 0, 0
+    for x in range(8):
+        for u in range(PU):
+            w, i = 0, 0
+            while True:
+                j = i * PU + ((PU - 1 - u) if i & 1 else u)
+                if j >= T8:
+                    break
+                W = x * T8 + j
+                g0 = (W // (hg * nqt)) * hg
+                level = (W - g0 * nqt) // min(hg, BH - g0)
+                q0 = ((nqt - 1 - level) if causal else level) * 256
+                w += ((min(q0 + 256 + off, Nk) if causal else Nk) + 63) // 64
+                i += 1
+            tot += w
+            worst = max(worst, w)
+    return "fa_fwd_persist_kernel" if worst * 8 * PU * 50 <= tot * 51 else "fa_fwd_kernel"
 
 
 def check_parity(cfg, inp, outs, slices=None):

@@ -1084,6 +1084,57 @@ static int cu_count() {
   return n > 0 ? n : 0;
 }
 
+// Whether the persistent kernel's fixed split of causal items is balanced
+// for this launch: the host replays the kernel's assignment (workgroup u of
+// the PU on XCD x takes positions i PU + u, i even, and i PU + PU - 1 - u,
+// i odd, of XCD x's share of map_tile's order) and compares the largest
+// workgroup's key tiles with the mean. The zigzag pairs heavy with light
+// items when a share's rows of PU positions fall on whole levels of the
+// grouped order; where they do not (4x32x3072, 4x16x4200: largest
+// 1.59-1.74x the mean) the fixed split measured up to 18% slower than the
+// dispatcher. (Non-causal items are equal: both splits end after
+// ceil(items / CUs) of them.) Replays are memoised per thread (a launch
+// shape is usually repeated).
+static bool persist_balanced(const FwdParams& p, bool causal, int grid) {
+  struct Key {
+    int bh, nq, nk, hg, grid;
+    bool causal;
+  };
+  thread_local Key keys[4];
+  thread_local bool vals[4];
+  thread_local int used = 0, next = 0;
+  const int BH = p.B * p.Hq, nq = p.Nq, nk = p.Nk, hg = p.heads_per_group > 1 ? p.heads_per_group : 1;
+  for (int i = 0; i < used; ++i)
+    if (keys[i].bh == BH && keys[i].nq == nq && keys[i].nk == nk && keys[i].hg == hg && keys[i].grid == grid &&
+        keys[i].causal == causal)
+      return vals[i];
+  const int nqt = (nq + 255) / 256, total = nqt * BH, T8 = total / 8, PU = grid / 8, off = nk - nq;
+  long long sum = 0, worst = 0;
+  for (int x = 0; x < 8; ++x)
+    for (int u = 0; u < PU; ++u) {
+      long long w = 0;
+      for (int i = 0;; ++i) {
+        const int j = i * PU + ((i & 1) ? PU - 1 - u : u);
+        if (j >= T8) break;
+        const int W = x * T8 + j;
+        const int g0 = (W / (hg * nqt)) * hg, gh = BH - g0 < hg ? BH - g0 : hg;
+        const int level = (W - g0 * nqt) / gh;
+        const int q0 = (causal ? nqt - 1 - level : level) * 256;
+        const int kv_end = causal ? (q0 + 256 + off < nk ? q0 + 256 + off : nk) : nk;
+        w += (kv_end + 63) / 64;
+      }
+      sum += w;
+      worst = w > worst ? w : worst;
+    }
+  // at most 2% above the mean
+  const bool ok = worst * 8LL * PU * 50 <= sum * 51;
+  keys[next] = Key{BH, nq, nk, hg, grid, causal};
+  vals[next] = ok;
+  next = (next + 1) & 3;
+  used = used < 4 ? used + 1 : 4;
+  return ok;
+}
+
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED, int NW>
 static hipError_t launch_fwd_nw(FwdParams p, hipStream_t s) {
   p.num_q_tiles = (p.Nq + NW * 32 - 1) / (NW * 32);
@@ -1101,21 +1152,27 @@ static hipError_t launch_fwd_nw(FwdParams p, hipStream_t s) {
 // varlen batches (packed or paged K/V) of up to 64 sequences (the
 // longest-first ranking) with runs of at least 512 queries (config 5,
 // 512-query chunks over 2.4k-7.3k keys: -5%).
-// Dense 8-wave launches with at least kPersistMinItems items per CU run
-// persistent (one workgroup per CU streaming its items; bit-identical
-// outputs) when every item has at least two key tiles (Nk > 64, and
-// Nk >= Nq if causal), the item count splits evenly over the 8 XCDs and no
-// workgroup takes more than kPersistMaxItems items.
+// Dense launches from 4096 queries (2048 at head dim 128) with at least
+// kPersistMinItems 256-query items per CU run persistent (one workgroup per
+// CU streaming its items; bit-identical outputs) when every item has at
+// least two key tiles (Nk > 64, and Nk >= Nq if causal), the item count
+// splits evenly over the 8 XCDs, no workgroup takes more than
+// kPersistMaxItems items and, when causal, the fixed split is balanced
+// (persist_balanced).
+// At 2048 queries and head dim 128 the persistent kernel beat the 4-wave
+// grid (config-2 shape -3.7%, non-causal -4.5%, 8x16 heads -2%); at head
+// dim 64 it lost 1.7% there.
 template <typename T, int DP, bool CAUSAL, bool VARLEN, bool PAGED = false>
 static hipError_t launch_fwd(const FwdParams& p, hipStream_t s) {
   if constexpr (!VARLEN && !PAGED && DP >= 64) {
-    if (p.Nq >= 4096) {
+    if (p.Nq >= (DP >= 128 ? 2048 : 4096)) {
       const int total = ((p.Nq + 255) / 256) * p.B * p.Hq;
       const int grid = (cu_count() / 8) * 8;
       if (grid >= 8 && total >= kPersistMinItems * grid && total % 8 == 0 &&
-          (total / 8 + grid / 8 - 1) / (grid / 8) <= kPersistMaxItems && p.Nk > 64 && (!CAUSAL || p.Nk >= p.Nq))
+          (total / 8 + grid / 8 - 1) / (grid / 8) <= kPersistMaxItems && p.Nk > 64 && (!CAUSAL || p.Nk >= p.Nq) &&
+          (!CAUSAL || persist_balanced(p, CAUSAL, grid)))
         return launch_fwd_persist<T, DP, CAUSAL>(p, grid, s);
-      return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);
+      if (p.Nq >= 4096) return launch_fwd_nw<T, DP, CAUSAL, VARLEN, PAGED, 8>(p, s);
     }
   }
   if constexpr (VARLEN && DP >= 64) {

@@ -273,19 +273,25 @@ def _abi_fwd(q, k, v, causal, scale):
 
 
 @pytest.mark.parametrize("B,H,Nq,Nk,D,causal,dtype,layout", [
-    (4, 16, 4200, 4200, 128, True, torch.bfloat16, "bhnd"),   # 1088 items, ragged last query tile
-    (3, 24, 4096, 4096, 64, False, torch.float16, "bhnd"),    # 1152 items: 4 or 5 per workgroup
-    (4, 16, 4096, 4608, 128, True, torch.bfloat16, "bhnd"),   # Nk > Nq, bottom-right causal
-    (4, 16, 4200, 4200, 96, False, torch.bfloat16, "bhnd"),   # padded head dim
+    (4, 16, 4096, 4096, 128, True, torch.bfloat16, "bhnd"),   # 1024 items, 4 per workgroup
+    (4, 32, 2048, 2048, 128, True, torch.float16, "bhnd"),    # 2048 queries (config-2 shape)
+    (4, 64, 4200, 4200, 128, False, torch.bfloat16, "bhnd"),  # 4352 items, ragged last query tile
+    (4, 16, 4096, 4096, 64, False, torch.float16, "bhnd"),    # head dim 64
+    (4, 32, 2048, 2048, 96, False, torch.bfloat16, "bhnd"),   # padded head dim
     (4, 16, 4096, 4096, 128, True, torch.bfloat16, "bnhd"),   # rows strided by H * D
+    (3, 24, 4096, 4096, 64, False, torch.float16, "bhnd"),    # 1152 items: 4 or 5 per workgroup
+    (4, 16, 4200, 4200, 128, True, torch.bfloat16, "bhnd"),   # fixed split unbalanced: per-item kernel
+    (4, 16, 4096, 4608, 128, True, torch.bfloat16, "bhnd"),   # Nk > Nq (unbalanced): per-item kernel
     (2, 16, 4200, 4200, 128, True, torch.bfloat16, "bhnd"),   # 544 items: too few, per-item kernel
 ])
 def test_persistent_forward(gpu, B, H, Nq, Nk, D, causal, dtype, layout):
-    """Dense 8-wave launches with at least four (b, h, 256-row tile) items per
-    CU (1024 on MI355X) run one workgroup per CU that streams its items (the K/V tiles of consecutive
-    items through one double buffer, the next item's Q rows and first score
-    tile during the current item's last step, O and L stored one step late):
-    every row of every (b, h) written once and within the gate."""
+    """Dense launches from 4096 queries (2048 at head dim 128) with at least
+    four (b, h, 256-row tile) items per CU (1024 on MI355X) whose fixed split
+    is balanced run one workgroup per CU that streams its items (the K/V
+    tiles of consecutive items through one double buffer, the next item's Q
+    rows and first score tile during the current item's last step, O and L
+    stored one step late): every row of every (b, h) written once and within
+    the gate. The last three shapes take the per-item kernel instead."""
     print(f"case persistent forward {B}x{H} Nq={Nq} Nk={Nk} D={D} causal={causal} {dtype} {layout}", flush=True)
     g = torch.Generator().manual_seed(Nq + Nk + D)
     if layout == "bnhd":
