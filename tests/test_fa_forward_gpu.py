@@ -95,14 +95,23 @@ def test_grouped_tile_order_covers_every_tile(gpu, B, H, N, causal):
     of K/V (here 4-16 heads: 13 and 15 heads leave a partial last group, and
     13 * 8 = 104 or 13 * 12 = 156 tiles are or are not a multiple of the 8
     XCDs): every query row of every head must be computed exactly once, so
-    each (b, h) slice matches the oracle, forward and backward."""
+    each (b, h) slice matches the oracle, forward and backward (gradients
+    under the gradient gate: max-abs 2e-2 and mean-abs 2e-3, or within 1.5x
+    of the restated reference algorithm's own error)."""
     from lightserve_amd.kernels.flash_attention_backward import _flash_attention_backward, _flash_attention_forward_lse
+    from oracle.attention import flash_backward_tiled
+    from tests.gates import assert_grad_parity
     print(f"case grouped order {B}x{H}x{N} causal={causal}", flush=True)
     g = torch.Generator().manual_seed(12)
-    q, k, v, do = (torch.randn(B, H, N, 128, generator=g).to(torch.bfloat16).to(gpu) for _ in range(4))
+    qc, kc, vc, doc = (torch.randn(B, H, N, 128, generator=g).to(torch.bfloat16) for _ in range(4))
+    q, k, v, do = (t.to(gpu) for t in (qc, kc, vc, doc))
     o, lse = _flash_attention_forward_lse(q, k, v, causal)
     dq, dk, dv = _flash_attention_backward(do, q, k, v, o, lse, causal)
     torch.cuda.synchronize()
+    # the reference's algorithm (bf16 rounding points), on the host, from the
+    # closed-form forward
+    o_cf, l_cf = attention_reference(qc, kc, vc, causal, dtype=torch.float32)
+    ref_alg = flash_backward_tiled(qc, kc, vc, o_cf.to(torch.bfloat16), l_cf, doc, causal, op_dtype=torch.bfloat16)
     from tests.test_fa_backward_gpu import _grads_gpu_fp32
     for b in range(B):
         for h in range(H):
@@ -110,10 +119,9 @@ def test_grouped_tile_order_covers_every_tile(gpu, B, H, N, causal):
             o_ref, l_ref = attention_reference(q[sl].float(), k[sl].float(), v[sl].float(), causal, dtype=torch.float32)
             assert_gate(o[sl].float(), o_ref, f"o (b={b},h={h})")
             assert_lse(lse[sl], l_ref, f"lse (b={b},h={h})")
-            ref = _grads_gpu_fp32(q[sl], k[sl], v[sl], do[sl], causal)
-            for name, got, want in zip(("dq", "dk", "dv"), (dq[sl], dk[sl], dv[sl]), ref):
-                err = (got.float() - want.float()).abs()
-                assert err.max().item() <= 5e-2 and err.mean().item() <= 2e-3, (name, b, h, err.max().item())
+            exact = _grads_gpu_fp32(q[sl], k[sl], v[sl], do[sl], causal)
+            for name, got, want, ra in zip(("dq", "dk", "dv"), (dq[sl], dk[sl], dv[sl]), exact, ref_alg):
+                assert_grad_parity(got.float().cpu(), want.float().cpu(), ra[sl], f"grouped {name} (b={b},h={h})")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
