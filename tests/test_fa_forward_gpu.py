@@ -313,3 +313,34 @@ def test_persistent_forward(gpu, B, H, Nq, Nk, D, causal, dtype, layout):
     o_ref, lse_ref = _oracle_gpu_chunked(q.float(), k.float(), v.float(), causal, heads_per_chunk=4)
     assert_gate(o.float(), o_ref, f"persistent {Nq}x{Nk} o")
     assert_lse(lse, lse_ref, f"persistent {Nq}x{Nk}")
+
+
+@pytest.mark.parametrize("B,H,Nq,Nk,D,causal,dtype,scale", [
+    (12, 8, 4096, 4096, 64, True, torch.bfloat16, -0.125),           # negative sm_scale
+    (5, 32, 2304, 3081, 128, False, torch.float16, 128 ** -0.5),     # Nk > Nq, ragged key tail
+    (6, 16, 3072, 3136, 128, True, torch.float16, 128 ** -0.5),      # causal with Nk > Nq
+    (6, 16, 3072, 3072, 128, False, torch.float16, -(128 ** -0.5)),  # negative sm_scale, head dim 128
+    (3, 32, 4160, 3860, 128, True, torch.bfloat16, 0.0442),          # causal Nk < Nq: rows that see no key
+    (16, 8, 4352, 4416, 96, True, torch.bfloat16, 96 ** -0.5),       # padded head dim
+    (3, 32, 4160, 8320, 128, False, torch.bfloat16, 128 ** -0.5),    # Nk = 2 Nq
+    (6, 16, 8192, 16384, 64, True, torch.float16, -0.125),           # long keys, negative sm_scale
+])
+def test_dense_forward_random_shapes(gpu, B, H, Nq, Nk, D, causal, dtype, scale):
+    """Seeded shapes around the persistent kernel's dispatch limits (item
+    counts per CU, balanced or not, Nq != Nk both ways, ragged tails, padded
+    head dims, any sm_scale): whichever kernel the host picks, every row is
+    written once and O / L pass the gate against the oracle."""
+    print(f"case dense forward {B}x{H} Nq={Nq} Nk={Nk} D={D} causal={causal} {dtype} scale={scale:.4f}", flush=True)
+    g = torch.Generator().manual_seed(Nq * 7 + Nk + D)
+    q = torch.randn(B, H, Nq, D, generator=g).to(dtype).to(gpu)
+    k, v = (torch.randn(B, H, Nk, D, generator=g).to(dtype).to(gpu) for _ in range(2))
+    o, lse = _abi_fwd(q, k, v, causal, scale)
+    assert not torch.isnan(o).any() and not torch.isnan(lse).any(), "a row was left unwritten"
+    o_ref = torch.empty(o.shape, device=gpu, dtype=torch.float32)
+    lse_ref = torch.empty(lse.shape, device=gpu, dtype=torch.float32)
+    for b in range(B):
+        for h0 in range(0, H, 4):
+            sl = (b, slice(h0, h0 + 4))
+            o_ref[sl], lse_ref[sl] = attention_reference(q[sl], k[sl], v[sl], causal, scale, dtype=torch.float32)
+    assert_gate(o.float(), o_ref, f"dense {Nq}x{Nk} o")
+    assert_lse(lse, lse_ref, f"dense {Nq}x{Nk}")
