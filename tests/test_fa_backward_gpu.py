@@ -268,15 +268,16 @@ def _random_case(seed):
     return B, H, Nq, Nk, D, dtype, r.random() < 0.5
 
 
-def _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, seed, what, flags=0):
+def _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, seed, what, flags=0, scale=None):
     """Forward with L and backward through the C ABI (workspace poisoned with
-    NaN bytes; lsfa_bwd_args.flags = flags) against the oracle: L and o under
-    the forward gate (rows that see no key: L = -inf, o = 0), dQ/dK/dV against
-    the float64 autograd under the gradient gate."""
+    NaN bytes; lsfa_bwd_args.flags = flags; sm_scale = scale, 1/sqrt(D) when
+    None) against the oracle: L and o under the forward gate (rows that see
+    no key: L = -inf, o = 0), dQ/dK/dV against the float64 autograd under the
+    gradient gate."""
     g = torch.Generator().manual_seed(1000 + seed)
     q, do = (torch.randn(B, H, Nq, D, generator=g).to(dtype) for _ in range(2))
     k, v = (torch.randn(B, H, Nk, D, generator=g).to(dtype) for _ in range(2))
-    scale = D ** -0.5
+    scale = D ** -0.5 if scale is None else scale
     o, L, dq, dk, dv = _abi_fwd_bwd(*(t.to(gpu) for t in (q, k, v, do)), causal, scale, phases=(flags,),
                                     poison=True)
     torch.cuda.synchronize()
@@ -314,6 +315,20 @@ def test_random_fwd_bwd(gpu, seed):
     B, H, Nq, Nk, D, dtype, causal = _random_case(seed)
     print(f"case random bwd seed={seed} {B}x{H} Nq={Nq} Nk={Nk} D={D} {dtype} causal={causal}", flush=True)
     _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, seed, f"seed {seed}")
+
+
+@pytest.mark.parametrize("B,H,Nq,Nk,D,causal,dtype,scale", [
+    (2, 3, 700, 700, 128, True, torch.bfloat16, -(128 ** -0.5)),  # negative sm_scale
+    (1, 2, 500, 900, 64, True, torch.float16, -0.05),              # negative, causal Nk > Nq
+    (1, 2, 900, 400, 96, True, torch.bfloat16, 0.25),              # larger than 1/sqrt(D), rows that see no key
+    (2, 2, 640, 640, 128, False, torch.float16, 0.02),             # small scale
+])
+def test_fwd_bwd_sm_scale(gpu, B, H, Nq, Nk, D, causal, dtype, scale):
+    """sm_scale other than 1/sqrt(D), negative included (the forward negates q
+    on load to keep its exponent scale positive; the backward's P, dK and dQ
+    carry the sign), through the C ABI against the oracle."""
+    print(f"case sm_scale bwd {B}x{H} Nq={Nq} Nk={Nk} D={D} {dtype} causal={causal} scale={scale}", flush=True)
+    _check_fwd_bwd(gpu, B, H, Nq, Nk, D, dtype, causal, Nq + Nk + D, f"scale {scale}", scale=scale)
 
 
 @pytest.mark.parametrize("Nq,Nk,causal,dtype", [(4160, 4160, True, torch.bfloat16), (4100, 700, True, torch.float16),
